@@ -1,0 +1,312 @@
+"""Decode throughput of the paged-attention engine on one MI355X.
+
+Workload (the decode-throughput configuration): GPT-2 124M, random-init fp32
+weights (normal std 0.02), 256 concurrent sequences whose context at the last
+timed step is ~ U[256, 1024] (seeded), block size 16, KV pool of 16,384 blocks
+(262,144 slots, 18 GiB). Prompts of random token ids are prefilled through the
+engine (untimed); then W warm-up and K timed decode steps run through
+``Engine.step`` (scheduler + paged forward + sampling + the step's one sync).
+
+Prints one JSON line: decode tok/s (``value``), the decode-attention kernel's
+roofline (algorithmic bytes / live HIP-event kernel time vs 8 TB/s), the
+CPU baseline (the oracle's restatement of the reference gather path on this
+host's cores, a bounded sample of the same state) and, unless ``--no-itl``,
+p50/p99 inter-token latency of the 300-request Poisson serving trace.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import random
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "decode tok/s (1 GPU); paged-attn HBM GB/s as % of peak; p50 ITL"
+HBM_PEAK_GBS = 8000.0
+N_SEQS, CTX_LO, CTX_HI, BLOCK, POOL_BLOCKS = 256, 256, 1024, 16, 16384
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def decode_bytes(ctxs: list[int], n_head: int = 12, d: int = 64, bs: int = BLOCK) -> int:
+    """Algorithmic HBM bytes of one decode-attention layer call: every cached K and V row once,
+    q in and out, the block-table entries and context lengths."""
+    kv = sum(2 * c * n_head * d * 4 for c in ctxs)
+    qo = 2 * len(ctxs) * n_head * d * 4
+    meta = sum(-(-c // bs) * 4 for c in ctxs) + 4 * len(ctxs)
+    return kv + qo + meta
+
+
+class KernelTimer:
+    """Brackets every tq_paged_decode call of the timed steps with HIP events on the launch stream."""
+
+    def __init__(self):
+        import torch
+
+        self.torch = torch
+        self.pairs = []
+        self.bytes = 0
+
+    def __call__(self, batch, phase):
+        if phase == "before":
+            ev = self.torch.cuda.Event(enable_timing=True)
+            ev.record()
+            self.pairs.append([ev, None])
+            self.bytes += decode_bytes([batch.context_lens[b] for b in range(batch.B) if batch.new_lens[b] == 1])
+        else:
+            ev = self.torch.cuda.Event(enable_timing=True)
+            ev.record()
+            self.pairs[-1][1] = ev
+
+    def total_ms(self) -> float:
+        return sum(a.elapsed_time(b) for a, b in self.pairs)
+
+
+def build_engine(steps_needed: int, seed: int = 0):
+    import torch
+
+    from tokquay_amd.engine import Engine
+    from tokquay_amd.kv_cache import BlockAllocator
+    from tokquay_amd.model import GPT2, GPT2Config
+    from tokquay_amd.scheduler import SchedulerConfig
+    from tokquay_amd.sequence import SamplingParams
+    from tokquay_amd.weights import random_state_dict
+
+    cfg = GPT2Config()
+    model = GPT2(cfg)
+    model.load_state_dict(random_state_dict(cfg, seed=seed))
+    model = model.cuda().eval()
+    alloc = BlockAllocator(cfg, POOL_BLOCKS, BLOCK, device="cuda")
+    engine = Engine(model, alloc, SchedulerConfig(max_num_seqs=N_SEQS, max_num_batched_tokens=32768, max_model_len=1024))
+    rng = random.Random(seed + 4)
+    final_ctx = [rng.randint(CTX_LO, CTX_HI) for _ in range(N_SEQS)]
+    for c in final_ctx:
+        prompt = [rng.randrange(50256) for _ in range(max(1, c - steps_needed))]
+        engine.add_request(prompt, SamplingParams(max_tokens=steps_needed + 2, ignore_eos=True))
+    t0 = time.perf_counter()
+    while engine.scheduler.waiting:
+        engine.step()  # prefill steps (and a few decodes between them)
+    torch.cuda.synchronize()
+    log(f"prefilled {N_SEQS} sequences in {time.perf_counter() - t0:.2f} s")
+    return engine, model
+
+
+def snapshot_for_cpu(engine, seqs, n_cpu: int, spare_per_seq: int):
+    """Copy the first n_cpu running sequences' blocks into a compact CPU pool (oracle layout),
+    with ``spare_per_seq`` empty blocks each for the positions the CPU steps append."""
+    import torch
+
+    pool = engine.allocator.pool
+    picked = seqs[:n_cpu]
+    used = sorted({b for s in picked for b in s.block_table})
+    remap = {b: i for i, b in enumerate(used)}
+    cpu_pool = torch.empty((len(used) + spare_per_seq * len(picked),) + tuple(pool.shape[1:]), dtype=pool.dtype)
+    for i in range(0, len(used), 512):
+        idx = torch.tensor(used[i : i + 512], device=pool.device)
+        cpu_pool[i : i + len(idx)].copy_(pool.index_select(0, idx))
+    spare = iter(range(len(used), cpu_pool.shape[0]))
+    state = []
+    for s in picked:
+        table = [remap[b] for b in s.block_table] + [next(spare) for _ in range(spare_per_seq)]
+        state.append((table, s.num_cached_tokens, list(s.token_ids)))
+    return cpu_pool, state
+
+
+def cpu_baseline(cpu_pool, state, weights, steps: int):
+    """Time the oracle (the reference gather-and-attend path, restated) on this host's CPU cores."""
+    import torch
+
+    from oracle.gpt2_ref import RefConfig, build_ref_model
+    from oracle.paged_ref import RefPagedBatch
+
+    threads = torch.get_num_threads()
+    model = build_ref_model(RefConfig(), weights)
+    tables = [list(t) for t, _, _ in state]
+    cached = [c for _, c, _ in state]
+    tokens = [list(t) for _, _, t in state]
+    times, first_ids = [], None
+    for step in range(steps + 1):  # the first step is the warm-up
+        batch = RefPagedBatch(cpu_pool, BLOCK, tables, cached, [1] * len(cached))
+        ids = torch.tensor([[t[c]] for t, c in zip(tokens, cached)])
+        t0 = time.perf_counter()
+        with torch.no_grad():
+            logits = model(ids, batch, last_only=True)[:, 0]
+        nxt = logits.argmax(-1).tolist()
+        dt = time.perf_counter() - t0
+        if step == 0:
+            first_ids = nxt
+        else:
+            times.append(dt)
+        for i, t in enumerate(nxt):
+            tokens[i].append(t)
+            cached[i] += 1
+    med = statistics.median(times)
+    return {"step_s": med, "threads": threads, "first_ids": first_ids, "times": times}
+
+
+def itl_trace(seed: int = 0, rate: float = 8.0, n: int = 300):
+    import torch
+
+    from tokquay_amd.engine import Engine
+    from tokquay_amd.harness import run_trace, summarize
+    from tokquay_amd.kv_cache import BlockAllocator
+    from tokquay_amd.model import GPT2, GPT2Config
+    from tokquay_amd.scheduler import SchedulerConfig
+    from tokquay_amd.weights import random_state_dict
+    from tokquay_amd.workload import make_workload
+
+    cfg = GPT2Config()
+    model = GPT2(cfg)
+    model.load_state_dict(random_state_dict(cfg, seed=seed))
+    model = model.cuda().eval()
+    # Warm-up trace (untimed) so kernels and GEMM heuristics are ready.
+    warm = Engine(model, BlockAllocator(cfg, 1024, 16, device="cuda"))
+    run_trace(warm, make_workload(math.inf, 12, seed=999, prompt_len=(16, 128), output_len=(8, 16)))
+    del warm
+    torch.cuda.synchronize()
+    alloc = BlockAllocator(cfg, 1024, 16, device="cuda")
+    engine = Engine(model, alloc, SchedulerConfig(max_num_seqs=64, max_num_batched_tokens=2048))
+    res = run_trace(engine, make_workload(rate, n, seed=seed))
+    s = summarize(res, alloc.bytes_per_block // 16)
+    return {
+        "requests": s["requests"],
+        "rate_req_s": rate,
+        "throughput_tok_s": round(s["throughput_tok_s"], 1),
+        "itl_p50_ms": round(s["itl_ms"]["p50"], 3),
+        "itl_p99_ms": round(s["itl_ms"]["p99"], 3),
+        "ttft_p50_ms": round(s["ttft_ms"]["p50"], 2),
+        "decode_step_p50_ms": round(s["stalls"].get("decode_step_ms", {}).get("p50", float("nan")), 3),
+        "preemptions": s["stats"]["num_preemptions"],
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=16)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--partition-tokens", type=int, default=0, help="decode partition size (0: automatic)")
+    ap.add_argument("--cpu-seqs", type=int, default=256, help="sequences in the CPU baseline sample (0: skip)")
+    ap.add_argument("--cpu-steps", type=int, default=2, help="timed CPU baseline steps (after one warm-up)")
+    ap.add_argument("--no-itl", action="store_true", help="skip the 300-request serving trace")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from tokquay_amd import kv_cache
+    from tokquay_amd.weights import random_state_dict
+
+    torch.manual_seed(0)
+    steps_needed = args.warmup + args.steps
+    engine, model = build_engine(steps_needed)
+    engine.allocator.decode_partition_tokens = args.partition_tokens
+
+    for _ in range(args.warmup):
+        engine.step()
+    running = list(engine.scheduler.running)
+    assert len(running) == N_SEQS, f"{len(running)} sequences running, expected {N_SEQS}"
+
+    cpu_state = None
+    if args.cpu_seqs > 0:
+        t0 = time.perf_counter()
+        cpu_state = snapshot_for_cpu(engine, running, args.cpu_seqs, spare_per_seq=args.cpu_steps // 16 + 2)
+        log(f"copied {cpu_state[0].shape[0]} blocks for the CPU sample in {time.perf_counter() - t0:.1f} s")
+
+    timer = KernelTimer()
+    kv_cache.PagedBatch.decode_hook = timer
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    first_ids = None
+    for k in range(args.steps):
+        events = engine.step()
+        if k == 0:
+            first_ids = [e.token_id for e in events]
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    kv_cache.PagedBatch.decode_hook = None
+    engine.allocator.check_device_errors()
+    ms_per_step = elapsed * 1e3 / args.steps
+    tok_s = N_SEQS * args.steps / elapsed
+    n_launch = len(timer.pairs)
+    kern_ms = timer.total_ms() / n_launch
+    bytes_per_launch = timer.bytes / n_launch
+    achieved = bytes_per_launch / (kern_ms * 1e-3) / 1e9
+    log(f"decode: {ms_per_step:.3f} ms/step, {tok_s:.0f} tok/s; attention {kern_ms * 1e3:.1f} us/launch, "
+        f"{bytes_per_launch / 1e9:.3f} GB/launch, {achieved:.0f} GB/s")  # fmt: skip
+
+    result = {
+        "metric": METRIC,
+        "value": round(tok_s, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: random-init weights (seed 0), random token ids",
+        "config": {
+            "workload": "scaled decode: GPT-2 124M fp32, 256 concurrent sequences, context U[256,1024], "
+            "block_size 16, pool 16384 blocks (262144 slots)",
+            "num_seqs": N_SEQS,
+            "block_size": BLOCK,
+            "pool_blocks": POOL_BLOCKS,
+            "decode_partition_tokens": args.partition_tokens,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "tq_paged_decode (decode_partition_kernel + decode_merge_kernel)",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel_us": round(kern_ms * 1e3, 2),
+            "bytes_per_launch": int(bytes_per_launch),
+            "launches": n_launch,
+        },
+    }
+
+    if cpu_state is not None:
+        cpu_pool, state = cpu_state
+        log(f"CPU baseline: {len(state)} sequences, {args.cpu_steps} timed steps ...")
+        cb = cpu_baseline(cpu_pool, state, random_state_dict(model.cfg, seed=0), args.cpu_steps)
+        n = len(state)
+        match = sum(int(a == b) for a, b in zip(cb["first_ids"], first_ids[:n])) / n
+        result["cpu_baseline"] = {
+            "value": round(n / cb["step_s"], 2),
+            "unit": "tok/s",
+            "cores": cb["threads"],
+            "kind": "port",
+            "sample": f"{args.cpu_steps} decode steps (median, after 1 warm-up) of {n} of the 256 sequences from the "
+            f"same state, oracle gather-and-attend path in fp32 torch on {cb['threads']} threads "
+            f"({platform.processor() or platform.machine()})",
+            "step_s": round(cb["step_s"], 3),
+            "greedy_ids_match_gpu": match,
+        }
+        del cpu_pool
+    if not args.no_itl:
+        log("serving trace: 300 requests, Poisson 8 req/s ...")
+        result["itl"] = itl_trace()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,153 @@
+/*
+ * tokquay_amd.h - C ABI of the MI355X (gfx950) paged-attention library.
+ *
+ * The library replaces the three tensor-level steps of Tokquay's paged
+ * attention branch with hand-written HIP kernels:
+ *
+ *   tq_cache_write    scatter each new token's K/V rows into the block pool
+ *   tq_paged_decode   one-query-per-sequence attention straight off the pool
+ *   tq_paged_prefill  causal (chunked) prefill attention straight off the pool
+ *
+ * KV pool layout (identical to the reference's, bit for bit):
+ *
+ *   pool[num_blocks][num_layers][2][num_heads][block_size][head_dim]  fp32,
+ *   contiguous, dim 2: 0 = K, 1 = V.
+ *
+ * Logical position p of a sequence lives in block block_table[p / block_size]
+ * at offset p % block_size; its flat slot is
+ * block_table[p / block_size] * block_size + p % block_size.
+ *
+ * Conventions
+ *   - Every pointer is a device pointer unless its comment says otherwise.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *     Every entry point only enqueues work on `stream`; none synchronises.
+ *   - Row strides are in elements (floats), not bytes; the innermost
+ *     (head, dim) block of every q / k / v / out row must be contiguous.
+ *   - `d_error` may be NULL. When not NULL it must point to a device int32 the
+ *     caller zeroed; kernels OR TQ_DEVERR_* bits into it when they meet an
+ *     out-of-range block id, slot or length. Such an entry is skipped (the
+ *     kernel never reads or writes outside the pool), so the result for that
+ *     row is undefined but the launch is memory safe.
+ *   - Only head_dim == 64 is supported (GPT-2 family). block_size may be any
+ *     value in [1, 1024].
+ *   - Calls are not thread safe with respect to the same pool: the caller
+ *     (one engine thread) orders them on one stream.
+ */
+#ifndef TOKQUAY_AMD_H_
+#define TOKQUAY_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum tq_status {
+  TQ_OK = 0,
+  TQ_ERR_INVALID_ARGUMENT = 1, /* a null pointer, a negative size, a layer out of range ... */
+  TQ_ERR_UNSUPPORTED = 2,      /* a shape this build has no kernel for (head_dim != 64 ...) */
+  TQ_ERR_WORKSPACE = 3,        /* workspace missing or smaller than the *_workspace_size() asked for */
+  TQ_ERR_HIP = 4               /* the HIP runtime refused the launch */
+} tq_status;
+
+/* Bits a kernel ORs into *d_error. */
+#define TQ_DEVERR_BLOCK_ID 1   /* a block-table entry outside [0, num_blocks) */
+#define TQ_DEVERR_SLOT 2       /* a slot_mapping entry >= num_blocks * block_size */
+#define TQ_DEVERR_LENGTH 4     /* a context / query length the block table cannot hold */
+
+/* Human-readable name of a status code (static storage, never NULL). */
+const char* tq_status_string(tq_status status);
+
+/* Version of this ABI; bumped whenever a signature changes. */
+int32_t tq_abi_version(void);
+
+/* Message of the last TQ_ERR_HIP on the calling thread ("" if none). */
+const char* tq_last_hip_error(void);
+
+/*
+ * Cache write: for every token n in [0, num_tokens) with slot = slot_mapping[n] >= 0,
+ *   pool[slot / block_size][layer][0][h][slot % block_size][:] = k[n * k_row_stride + h * 64 + :]
+ *   pool[slot / block_size][layer][1][h][slot % block_size][:] = v[n * v_row_stride + h * 64 + :]
+ * for every head h. A negative slot marks a padded token, which writes nothing.
+ * The copy is bit exact.
+ *
+ * Replaces PagedBatch.write (tokquay/kv_cache.py:228-232) together with the
+ * scatter targets PagedBatch.__init__ builds for it (tokquay/kv_cache.py:216-226):
+ * slot_mapping[n] is block_table[p // block_size] * block_size + p % block_size
+ * for the token at position p (tokquay/kv_cache.py:9-10, :223-224).
+ */
+tq_status tq_cache_write(float* pool, int64_t num_blocks, int32_t num_layers, int32_t num_heads,
+                         int32_t block_size, int32_t head_dim, int32_t layer,
+                         const float* k, int64_t k_row_stride,
+                         const float* v, int64_t v_row_stride,
+                         const int64_t* slot_mapping, int64_t num_tokens,
+                         int32_t* d_error, void* stream);
+
+/*
+ * Paged decode attention: one query per sequence, attending to every cached
+ * position of that sequence (the query's own K/V must already be in the pool):
+ *
+ *   out[b, h, :] = softmax_j(scale * q[b, h, :] . K_b[h, j, :]) @ V_b[h, j, :],  j < context_lens[b]
+ *
+ * where K_b / V_b are read through block_tables[b * block_table_stride + j / block_size].
+ * q row b starts at q + b * q_row_stride (heads contiguous), out row b at
+ * out + b * out_row_stride. Rows with context_lens[b] == 0 get zeros.
+ * max_context_len must be >= every context_lens[b] (it sizes the grid).
+ *
+ * The kernel splits each sequence into partitions of partition_tokens
+ * positions (a multiple of 16; 0 = choose automatically) and merges them with
+ * a log-sum-exp pass when a sequence spans several. The merge needs
+ * tq_paged_decode_workspace_size(...) bytes of device workspace.
+ *
+ * Replaces PagedBatch.gather (tokquay/kv_cache.py:234-242), the mask it is used
+ * with (tokquay/kv_cache.py:208-214) and the attention math of
+ * Attention.forward (tokquay/model.py:94-96) for rows that feed one token.
+ */
+tq_status tq_paged_decode(float* out, int64_t out_row_stride,
+                          const float* q, int64_t q_row_stride,
+                          const float* pool, int64_t num_blocks, int32_t num_layers,
+                          int32_t num_heads, int32_t block_size, int32_t head_dim, int32_t layer,
+                          const int32_t* block_tables, int64_t block_table_stride,
+                          int32_t max_blocks_per_seq,
+                          const int32_t* context_lens, int32_t num_seqs, int32_t max_context_len,
+                          float scale, int32_t partition_tokens,
+                          void* workspace, size_t workspace_bytes,
+                          int32_t* d_error, void* stream);
+
+/* Bytes of workspace tq_paged_decode needs for these sizes (0 if none). */
+size_t tq_paged_decode_workspace_size(int32_t num_seqs, int32_t num_heads, int32_t head_dim,
+                                      int32_t max_context_len, int32_t partition_tokens);
+
+/*
+ * Paged prefill / chunked-prefill attention. Sequence b feeds
+ * n_b = cu_seqlens_q[b+1] - cu_seqlens_q[b] new tokens at positions
+ * q_start[b] .. q_start[b] + n_b - 1, whose q rows are
+ * q + (cu_seqlens_q[b] + i) * q_row_stride. Its K/V for positions
+ * [0, q_start[b] + n_b) must already be in the pool. Causal:
+ *
+ *   out[row, h, :] = softmax_{j <= q_start[b] + i}(scale * q[row, h, :] . K_b[h, j, :]) @ V_b[h, j, :]
+ *
+ * cu_seqlens_q has num_seqs + 1 entries, starts at 0 and is non-decreasing;
+ * num_q_rows is cu_seqlens_q[num_seqs] (the kernels reject rows beyond it).
+ * max_query_len >= every n_b (it sizes the grid).
+ *
+ * Replaces PagedBatch.gather + mask + Attention.forward's masked softmax
+ * (tokquay/kv_cache.py:208-214, :234-242; tokquay/model.py:94-96) for rows that
+ * feed several tokens (prefill, recompute after preemption, chunked prefill).
+ */
+tq_status tq_paged_prefill(float* out, int64_t out_row_stride,
+                           const float* q, int64_t q_row_stride,
+                           const float* pool, int64_t num_blocks, int32_t num_layers,
+                           int32_t num_heads, int32_t block_size, int32_t head_dim, int32_t layer,
+                           const int32_t* block_tables, int64_t block_table_stride,
+                           int32_t max_blocks_per_seq,
+                           const int32_t* cu_seqlens_q, const int32_t* q_start,
+                           int32_t num_seqs, int32_t num_q_rows, int32_t max_query_len,
+                           float scale, int32_t* d_error, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TOKQUAY_AMD_H_ */

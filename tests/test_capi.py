@@ -1,0 +1,82 @@
+"""The C-ABI library loads on a host without a GPU and exports every symbol the header declares.
+
+Only host-side argument checks are exercised here (they return before any HIP
+call); nothing is launched.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from tokquay_amd import _lib
+from tokquay_amd.build import LIB_PATH
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "tokquay_amd.h")
+
+
+def declared_functions() -> list[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tq_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB_PATH):
+        pytest.fail(f"{LIB_PATH} is not built (run __graft_entry__.build())")
+    return _lib.lib()
+
+
+def test_header_declares_the_three_kernels_and_helpers():
+    names = declared_functions()
+    for n in ("tq_cache_write", "tq_paged_decode", "tq_paged_prefill", "tq_paged_decode_workspace_size",
+              "tq_status_string", "tq_abi_version", "tq_last_hip_error"):  # fmt: skip
+        assert n in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    raw = ctypes.CDLL(LIB_PATH)
+    missing = [n for n in declared_functions() if not hasattr(raw, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    assert set(declared_functions()) == set(_lib.SIGNATURES), "ctypes bindings and header disagree"
+
+
+def test_status_strings_and_version(lib):
+    assert lib.tq_abi_version() == 1
+    assert lib.tq_status_string(0) == b"ok"
+    assert lib.tq_status_string(3) == b"workspace missing or too small"
+    assert lib.tq_last_hip_error() == b""
+
+
+def test_invalid_arguments_are_rejected_before_any_launch(lib):
+    # num_blocks = 0
+    assert lib.tq_cache_write(None, 0, 1, 12, 16, 64, 0, None, 768, None, 768, None, 1, None, None) == 1
+    # layer out of range
+    assert lib.tq_cache_write(None, 8, 2, 12, 16, 64, 2, None, 768, None, 768, None, 1, None, None) == 1
+    # head_dim 128 is not built
+    assert lib.tq_cache_write(None, 8, 2, 12, 16, 128, 0, None, 768, None, 768, None, 1, None, None) == 2
+    # zero tokens is a no-op
+    assert lib.tq_cache_write(None, 8, 2, 12, 16, 64, 0, None, 768, None, 768, None, 0, None, None) == 0
+    # decode: null pointers with sequences to do
+    assert lib.tq_paged_decode(None, 768, None, 768, None, 8, 1, 12, 16, 64, 0, None, 4, 4, None, 2, 64,
+                               0.125, 0, None, 0, None, None) == 1  # fmt: skip
+    # decode: partition not a multiple of 16
+    assert lib.tq_paged_decode(None, 768, None, 768, None, 8, 1, 12, 16, 64, 0, None, 4, 4, None, 2, 64,
+                               0.125, 24, None, 0, None, None) == 1  # fmt: skip
+    # prefill: zero sequences is a no-op
+    assert lib.tq_paged_prefill(None, 768, None, 768, None, 8, 1, 12, 16, 64, 0, None, 4, 4, None, None,
+                                0, 0, 0, 0.125, None, None) == 0  # fmt: skip
+
+
+def test_decode_workspace_size(lib):
+    # Contexts that fit one partition need no workspace.
+    assert lib.tq_paged_decode_workspace_size(64, 12, 64, 200, 256) == 0
+    # 256 sequences x 12 heads x 4 partitions of 256 x (64 + 4) floats.
+    assert lib.tq_paged_decode_workspace_size(256, 12, 64, 1024, 256) == 256 * 12 * 4 * 68 * 4
+    assert lib.tq_paged_decode_workspace_size(256, 12, 64, 1024, 0) == 256 * 12 * 4 * 68 * 4  # automatic: 256
+    assert lib.tq_paged_decode_workspace_size(4, 12, 64, 1024, 0) == 4 * 12 * 32 * 68 * 4  # small batch: 32
+    assert lib.tq_paged_decode_workspace_size(4, 12, 64, 1024, 20) == 0  # invalid partition

@@ -1,0 +1,153 @@
+"""GPU parity of the three kernels against the reference's gather-and-attend path.
+
+Bar: bit-exact pool after the cache write (it is a copy); fp32 attention
+outputs within 1e-5 relative / 1e-4 absolute of the reference path (CPU fp32)
+and of float64 brute-force attention.
+"""
+
+from __future__ import annotations
+
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from tests.paged_cases import ATOL, RTOL, Scenario, cdiv
+
+pytestmark = pytest.mark.gpu
+
+
+def check(sc: Scenario, partition_tokens: int = 0, brute: bool = True):
+    pool_ref, out_ref = sc.reference()
+    pool_gpu, out_gpu, batch = sc.run_product(partition_tokens)
+    assert torch.equal(pool_gpu, pool_ref), "pool differs from the reference scatter"
+    want = sc.packed_reference(out_ref, batch.token_index)
+    torch.testing.assert_close(out_gpu, want, rtol=RTOL, atol=ATOL)
+    if brute:
+        rows = batch.token_index.cpu().tolist()
+        exact = sc.brute_force(pool_ref)
+        T = sc.q.shape[2]
+        got = out_gpu.view(-1, 12, 64).double().numpy()
+        for r, flat in enumerate(rows):
+            b, t = divmod(flat, T)
+            np.testing.assert_allclose(got[r], exact[b][t], rtol=RTOL, atol=ATOL)
+    return out_gpu, batch
+
+
+# ------------------------------------------------------------------------------ decode
+def config2_contexts(seed: int = 0, num_blocks: int = 1024, block_size: int = 16) -> tuple[list[int], int]:
+    """64 context lengths ~ U[16, 512]; redrawn (seed, seed+1, ...) until they fit the 1024-block pool."""
+    s = seed
+    while True:
+        rng = random.Random(s)
+        ctx = [rng.randint(16, 512) for _ in range(64)]
+        if sum(cdiv(c, block_size) for c in ctx) <= num_blocks:
+            return ctx, s
+        s += 1
+
+
+@pytest.mark.parametrize("n_layer,layer", [(1, 0), (12, 7)])
+def test_decode_config2_op(n_layer, layer):
+    ctx, _ = config2_contexts()
+    sc = Scenario([c - 1 for c in ctx], [1] * len(ctx), block_size=16, n_layer=n_layer, layer=layer,
+                  num_blocks=1024, seed=11)  # fmt: skip
+    out, batch = check(sc)
+    assert batch.num_decode == 64 and batch.num_prefill == 0
+
+
+@pytest.mark.parametrize("block_size", [1, 4, 8, 16, 32])
+@pytest.mark.parametrize("partition_tokens", [0, 16, 64, 256])
+def test_decode_edge_contexts(block_size, partition_tokens):
+    ctx = [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 255, 256, 257, 511, 512, 1023, 1024]
+    sc = Scenario([c - 1 for c in ctx], [1] * len(ctx), block_size=block_size, seed=block_size)
+    check(sc, partition_tokens)
+
+
+def test_decode_config4_scale():
+    """256 sequences, contexts ~ U[256, 1024], block size 16 (the decode-throughput workload's shape)."""
+    rng = random.Random(4)
+    ctx = [rng.randint(256, 1024) for _ in range(256)]
+    sc = Scenario([c - 1 for c in ctx], [1] * 256, block_size=16, seed=4)
+    check(sc, brute=False)
+
+
+# ------------------------------------------------------------------------------ prefill
+@pytest.mark.parametrize("block_size", [4, 16])
+@pytest.mark.parametrize("start,n", [(0, 2), (0, 15), (0, 16), (0, 17), (0, 100), (5, 40), (16, 16), (250, 300), (0, 1024)])
+def test_prefill_single_sequence(block_size, start, n):
+    sc = Scenario([start], [n], block_size=block_size, seed=start * 7 + n)
+    check(sc)
+
+
+def test_prefill_batch_of_ragged_prompts():
+    lens = [1, 3, 7, 12, 16, 17, 33, 48]  # the reference's headline batch (tests/test_phase3_paged.py:113)
+    sc = Scenario([0] * len(lens), lens, block_size=16, seed=8)
+    out, batch = check(sc)
+    assert batch.num_decode == 1 and batch.num_prefill == 7
+
+
+@pytest.mark.parametrize("chunk", [0, 1, 2, 3])
+def test_mixed_chunked_prefill_and_decode(chunk):
+    """4 prompts of 512-1024 tokens fed in 256-token chunks (chunk k starts at 256k) next to 128
+    decoding sequences with contexts ~ U[64, 768]: one mixed step."""
+    rng = random.Random(5)
+    prompts = [rng.randint(512, 1024) for _ in range(4)]
+    dec_ctx = [rng.randint(64, 768) for _ in range(128)]
+    starts, lens = [], []
+    for p in prompts:
+        s = 256 * chunk
+        starts.append(s)
+        lens.append(max(1, min(256, p - s)))
+    starts += [c - 1 for c in dec_ctx]
+    lens += [1] * len(dec_ctx)
+    sc = Scenario(starts, lens, block_size=16, seed=50 + chunk)
+    check(sc, brute=False)
+
+
+# ------------------------------------------------------------------------------ contract edges
+def test_write_contract_padded_layout_is_bit_exact_and_padding_never_writes():
+    """BatchedKV.write with the reference's [B, H, T, d] layout: padded positions write nothing and
+    blocks nobody owns stay bit-identical (tests/test_phase3_paged.py:125-129)."""
+    from oracle.paged_ref import RefPagedBatch
+    from tokquay_amd.kv_cache import PagedBatch
+
+    sc = Scenario([0, 3, 20, 0], [5, 1, 9, 13], block_size=4, num_blocks=40, seed=21)
+    pool_ref = sc.pool.clone()
+    RefPagedBatch(pool_ref, 4, sc.tables, sc.starts, sc.new_lens).write(0, sc.k, sc.v)
+    pool = sc.pool.cuda()
+    PagedBatch(pool, 4, sc.tables, sc.starts, sc.new_lens).write(0, sc.k.cuda(), sc.v.cuda())
+    assert torch.equal(pool.cpu(), pool_ref)
+    owned = {b for t in sc.tables for b in t}
+    untouched = [b for b in range(sc.num_blocks) if b not in owned]
+    assert untouched and torch.equal(pool.cpu()[untouched], sc.pool[untouched])
+
+
+def test_out_of_range_block_id_is_reported_not_followed():
+    """A block id past the pool is caught by the kernels' bounds check and reported."""
+    from tokquay_amd import ops
+
+    pool = torch.zeros(8, 1, 2, 12, 16, 64, device="cuda")
+    q = torch.randn(2, 12, 64, device="cuda")
+    out = torch.empty_like(q)
+    tables = torch.tensor([[0, 1], [2, 8 + 5]], dtype=torch.int32, device="cuda")
+    ctx = torch.tensor([20, 20], dtype=torch.int32, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ops.paged_decode(out, q, pool, 0, tables, ctx, 20, d_error=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) & 1
+    assert torch.isfinite(out).all()
+
+
+def test_host_side_argument_errors_raise():
+    from tokquay_amd import _lib, ops
+
+    pool = torch.zeros(4, 1, 2, 12, 16, 64, device="cuda")
+    q = torch.randn(1, 12, 64, device="cuda")
+    tables = torch.zeros(1, 4, dtype=torch.int32, device="cuda")
+    ctx = torch.tensor([1000], dtype=torch.int32, device="cuda")
+    tiny = torch.empty(16, dtype=torch.uint8, device="cuda")
+    with pytest.raises(_lib.KernelError, match="workspace"):
+        ops.paged_decode(torch.empty_like(q), q, pool, 0, tables, ctx, 1000, partition_tokens=16, workspace=tiny)
+    with pytest.raises(ValueError):
+        ops.paged_decode(torch.empty_like(q), q, pool, 1, tables, ctx, 1000)  # layer out of range

@@ -1,0 +1,166 @@
+"""End-to-end GPU parity: the engine on the HIP path emits the reference's greedy tokens.
+
+The reference is the oracle's restatement of the reference model and drivers,
+run in fp32 on the CPU with the same deterministic random-init weights.
+"""
+
+from __future__ import annotations
+
+import random
+
+import pytest
+import torch
+
+from oracle.gpt2_ref import RefAllocator, RefConfig, build_ref_model, ref_greedy_generate, ref_paged_greedy_generate
+from tokquay_amd.engine import Engine
+from tokquay_amd.generate import paged_greedy_generate
+from tokquay_amd.kv_cache import BlockAllocator
+from tokquay_amd.model import GPT2, GPT2Config
+from tokquay_amd.scheduler import SchedulerConfig
+from tokquay_amd.sequence import SamplingParams, SequenceStatus
+from tokquay_amd.weights import random_state_dict
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def weights():
+    return random_state_dict(GPT2Config(), seed=0)
+
+
+@pytest.fixture(scope="module")
+def gpu_model(weights):
+    m = GPT2(GPT2Config())
+    m.load_state_dict(weights)
+    return m.cuda().eval()
+
+
+@pytest.fixture(scope="module")
+def ref_model(weights):
+    return build_ref_model(RefConfig(), weights)
+
+
+_memo: dict = {}
+
+
+def reference(ref_model, prompt, n):
+    key = (tuple(prompt), n)
+    if key not in _memo:
+        _memo[key] = ref_greedy_generate(ref_model, list(prompt), n)
+    return _memo[key]
+
+
+def config1_prompts(seed: int = 1) -> list[list[int]]:
+    """8 prompts, lengths ~ U[16, 64], ids ~ U[0, 50255] (EOS avoided)."""
+    rng = random.Random(seed)
+    return [[rng.randrange(50256) for _ in range(rng.randint(16, 64))] for _ in range(8)]
+
+
+@pytest.mark.parametrize("hard", [False, True])
+def test_config1_greedy_ids_identical(gpu_model, ref_model, hard):
+    prompts = config1_prompts()
+    margins: list[float] = []
+    want = ref_paged_greedy_generate(ref_model, RefAllocator(RefConfig(), 256, 16), prompts, 32, margins)
+    alloc = BlockAllocator(gpu_model.cfg, 256, 16, device="cuda")
+    if hard:  # garbage pool + shuffled free list
+        g = torch.Generator().manual_seed(3)
+        alloc.pool.copy_(torch.randn(alloc.pool.shape, generator=g) * 50)
+        random.Random(3).shuffle(alloc._free)
+    got = paged_greedy_generate(gpu_model, alloc, prompts, 32)
+    alloc.check_device_errors()
+    print(f"\nsmallest top-1/top-2 logit margin over {len(margins)} picks: {min(margins):.3e}")
+    assert got == want
+    assert alloc.num_free_blocks == alloc.num_blocks
+
+
+def greedy(n):
+    return SamplingParams(max_tokens=n, ignore_eos=True)
+
+
+def run(engine, arrivals, max_steps=5000):
+    pending = sorted(arrivals, key=lambda a: a[0])
+    seqs = []
+    for step in range(max_steps):
+        while pending and pending[0][0] <= step:
+            _, prompt, params = pending.pop(0)
+            seqs.append(engine.add_request(prompt, params))
+        if not pending and not engine.has_unfinished():
+            return seqs
+        engine.step()
+    pytest.fail("engine did not finish")
+
+
+def text(seed, n):
+    rng = random.Random(seed)
+    return [rng.randrange(50256) for _ in range(n)]
+
+
+def test_staggered_arrivals_match_reference(gpu_model, ref_model):
+    specs = [(0, text(1, 5), 30), (0, text(2, 30), 12), (3, text(3, 8), 25), (6, text(4, 1), 20),
+             (6, text(5, 33), 15), (11, text(6, 17), 18)]  # fmt: skip
+    engine = Engine(gpu_model, BlockAllocator(gpu_model.cfg, 256, 16, device="cuda"))
+    seqs = run(engine, [(t, p, greedy(n)) for t, p, n in specs])
+    for seq, (_, prompt, n) in zip(seqs, specs):
+        assert seq.output_token_ids == reference(ref_model, prompt, n)
+    assert engine.stats.max_batch >= 3
+
+
+def test_tiny_pool_preemption_still_matches_reference(gpu_model, ref_model):
+    specs = [(0, text(10 + i, 20 + 5 * i), 40 + 4 * i) for i in range(8)]
+    engine = Engine(gpu_model, BlockAllocator(gpu_model.cfg, 16, 16, device="cuda"))
+    seqs = run(engine, [(t, p, greedy(n)) for t, p, n in specs])
+    assert engine.stats.num_preemptions > 0
+    for seq, (_, prompt, n) in zip(seqs, specs):
+        assert seq.status is SequenceStatus.FINISHED
+        assert seq.output_token_ids == reference(ref_model, prompt, n)
+    assert engine.allocator.num_free_blocks == 16
+
+
+def test_mixed_prefill_and_decode_step_matches_full_forward(gpu_model, ref_model):
+    """One step where A decodes one token while B prefills its whole prompt (tests/test_phase3_paged.py:143-164)."""
+    from tokquay_amd.generate import paged_forward
+    from tokquay_amd.sequence import Sequence
+
+    a_ids, b_ids = text(31, 14), text(32, 23)
+    alloc = BlockAllocator(gpu_model.cfg, 64, 4, device="cuda")
+    a = Sequence(0, a_ids[:-1])
+    alloc.allocate(a)
+    paged_forward(gpu_model, alloc, [a])
+    a.append_token(a_ids[-1])
+    alloc.append_slot(a)
+    b = Sequence(1, b_ids)
+    alloc.allocate(b)
+    logits = paged_forward(gpu_model, alloc, [a, b]).cpu()
+    with torch.no_grad():
+        full_a = ref_model(torch.tensor([a_ids]))[0, -1]
+        full_b = ref_model(torch.tensor([b_ids]))[0, -1]
+    torch.testing.assert_close(logits[0], full_a, rtol=1e-3, atol=1e-3)
+    torch.testing.assert_close(logits[1], full_b, rtol=1e-3, atol=1e-3)
+
+
+def test_chunked_prefill_equals_one_shot_prefill(gpu_model):
+    """Feeding a prompt in chunks (new_lens) gives the same logits as one prefill."""
+    from tokquay_amd.generate import paged_forward
+    from tokquay_amd.sequence import Sequence
+
+    prompt = text(41, 700)
+    alloc = BlockAllocator(gpu_model.cfg, 128, 16, device="cuda")
+    one = Sequence(0, prompt)
+    alloc.allocate(one)
+    want = paged_forward(gpu_model, alloc, [one])
+    chunked = Sequence(1, prompt)
+    alloc.allocate(chunked)
+    for n in (256, 256, 188):
+        got = paged_forward(gpu_model, alloc, [chunked], [n])
+    torch.testing.assert_close(got, want, rtol=1e-3, atol=1e-3)
+
+
+def test_stats_and_idle_engine(gpu_model):
+    engine = Engine(gpu_model, BlockAllocator(gpu_model.cfg, 64, 16, device="cuda"), SchedulerConfig())
+    for i in range(3):
+        engine.add_request(text(50 + i, 9), greedy(6))
+    engine.run_until_done()
+    st = engine.stats
+    assert st.tokens_generated == 18 and st.max_batch == 3
+    assert st.prefill_steps == 1 and st.decode_steps == 5
+    assert engine.step() == []

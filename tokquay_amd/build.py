@@ -1,0 +1,68 @@
+"""Builds ``libtokquay_amd.so`` (the gfx950 kernels and their C ABI) in place.
+
+Run ``python -m tokquay_amd.build``. The library is compiled straight with
+``hipcc`` for gfx950 only; it has no torch dependency, so any host program can
+load it through ``include/tokquay_amd.h``.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PKG_DIR)
+CSRC_DIR = os.path.join(PKG_DIR, "csrc")
+INCLUDE_DIR = os.path.join(REPO_DIR, "include")
+LIB_NAME = "libtokquay_amd.so"
+LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+OFFLOAD_ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={OFFLOAD_ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    # Packed fp32 VALU ops (v_pk_*_f32) are kept out of every kernel.
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    "-Wall",
+]
+
+
+def sources() -> list[str]:
+    return sorted(os.path.join(CSRC_DIR, f) for f in os.listdir(CSRC_DIR) if f.endswith(".hip"))
+
+
+def hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(path):
+        raise RuntimeError("hipcc not found (ROCm is required to build the kernels)")
+    return path
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every kernel source into LIB_PATH and return that path."""
+    tmp = LIB_PATH + ".tmp"
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", "-o", tmp, *sources()]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    # The host compiler pass does not know the packed-fp32 target feature and says so; that is expected.
+    noise = ("packed-fp32-ops", "not a recognized feature", "warning generated", "warnings generated")
+    msgs = [ln for ln in (proc.stdout + proc.stderr).splitlines() if ln.strip() and not any(n in ln for n in noise)]
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n" + "\n".join(msgs))
+    if verbose and msgs:
+        print("\n".join(msgs), flush=True)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose="-q" not in sys.argv[1:]))

@@ -1,0 +1,374 @@
+// Paged decode attention for gfx950: one query token per sequence, K/V read
+// in place from the block pool (no gathered copy), online softmax, no MFMA.
+//
+// Decode attention is a GEMV (0.5 flop per byte), so the kernel is built to
+// stream the pool at HBM speed:
+//   * one 64-lane wave per (sequence, head, partition); 4 waves (4 adjacent
+//     heads, whose tiles sit next to each other in the pool) per workgroup;
+//   * a chunk of 16 positions is read as 4 float4 loads per lane for K and 4
+//     for V. Lane i reads dims 4*(i%16)..+3 of position t0 + 4j + i/16, so
+//     each load instruction covers 1 KiB of a contiguous (block, layer, kv,
+//     head) tile and every 16-lane DPP row holds one position;
+//   * q.k is a 4-term dot product per lane plus a 16-lane DPP reduction
+//     (no LDS traffic);
+//   * each DPP row keeps its own running max / sum / accumulator over the
+//     positions it owns, so the loop has no cross-row communication; the four
+//     rows are merged once at the end (xor-16 / xor-32 shuffles);
+//   * the next chunk's 8 loads are issued before the current chunk's math.
+// Long contexts are cut into partitions of `part_tokens` positions to fill the
+// 256 CUs; a second small kernel merges the partitions (log-sum-exp).
+//
+// Reference semantics: PagedBatch.gather + mask (tokquay/kv_cache.py:208-214,
+// :234-242) and the masked softmax attention of Attention.forward
+// (tokquay/model.py:94-96), for a query at position ctx-1 that sees keys
+// 0..ctx-1 (tokquay/kv_cache.py:188, :213-214).
+
+#include <math.h>
+
+#include "tq_internal.h"
+
+namespace tq {
+namespace {
+
+constexpr int kHeadsPerGroup = 4;               // waves (heads) per workgroup
+constexpr int kChunk = 16;                      // positions per loop iteration
+constexpr int kPartialStride = kHeadDim + 4;    // acc[64], m, l, 2 pad: 16-byte aligned rows
+
+struct DecodeArgs {
+  float* out;
+  int64_t out_stride;
+  const float* q;
+  int64_t q_stride;
+  const float* pool_layer;  // pool + layer offset
+  int64_t block_stride;
+  int64_t kv_stride;
+  int64_t head_stride;
+  const int32_t* block_tables;
+  int64_t bt_stride;
+  const int32_t* context_lens;
+  float* partials;  // [num_seqs][num_heads][max_parts][kPartialStride]
+  int32_t* d_error;
+  float scale;
+  int32_t num_blocks;
+  int32_t num_heads;
+  int32_t block_size;
+  int32_t ctx_cap;  // min(max_blocks * block_size, max_parts * part_tokens)
+  int32_t part_tokens;
+  int32_t max_parts;
+};
+
+__device__ __forceinline__ int load_context(const DecodeArgs& a, int b, bool report) {
+  int ctx = a.context_lens[b];
+  if (ctx < 0 || ctx > a.ctx_cap) {
+    if (report) flag_error(a.d_error, TQ_DEVERR_LENGTH);
+    ctx = ctx < 0 ? 0 : a.ctx_cap;
+  }
+  return ctx;
+}
+
+// Loads positions t0 + 4j + r (j = 0..3) of this lane's DPP row r into registers.
+// Branch free: every lane loads from an in-bounds address (positions past
+// t_end re-read a position of the same block, bad block ids read block 0) and
+// invalid positions are zeroed by a select and reported through ok[j].
+template <int BS_CT>
+__device__ __forceinline__ void load_chunk(const DecodeArgs& a, const int32_t* bt,
+                                           const float* head_base, int bs, int t0, int t_end,
+                                           int r, float4 (&kx)[4], float4 (&vx)[4], bool (&ok)[4]) {
+  const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+  if constexpr (BS_CT >= kChunk) {
+    // The whole chunk sits in one block (t0 is a multiple of 16 and so is BS_CT),
+    // and t0 < t_end, so bt[t0 / BS_CT] is inside the table row.
+    int64_t blk = bt[t0 / BS_CT];
+    const bool blk_ok = (uint64_t)blk < (uint64_t)a.num_blocks;
+    if (!blk_ok) {
+      if ((threadIdx.x & 63) == 0) flag_error(a.d_error, TQ_DEVERR_BLOCK_ID);
+      blk = 0;
+    }
+    const float* base = head_base + blk * a.block_stride + (int64_t)(t0 % BS_CT) * kHeadDim;
+    float4 k_raw[4], v_raw[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float* p = base + (4 * j + r) * kHeadDim;
+      k_raw[j] = *reinterpret_cast<const float4*>(p);
+      v_raw[j] = *reinterpret_cast<const float4*>(p + a.kv_stride);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      ok[j] = blk_ok && (t0 + 4 * j + r < t_end);
+      kx[j] = ok[j] ? k_raw[j] : zero;
+      vx[j] = ok[j] ? v_raw[j] : zero;
+    }
+  } else {
+    float4 k_raw[4], v_raw[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t_req = t0 + 4 * j + r;
+      const int t = t_req < t_end ? t_req : t_end - 1;  // t_end > t0 >= 0
+      const int bi = t / bs;
+      int64_t blk = bt[bi];
+      const bool blk_ok = (uint64_t)blk < (uint64_t)a.num_blocks;
+      if (!blk_ok) {
+        flag_error(a.d_error, TQ_DEVERR_BLOCK_ID);
+        blk = 0;
+      }
+      ok[j] = blk_ok && t_req < t_end;
+      const float* p = head_base + blk * a.block_stride + (int64_t)(t - bi * bs) * kHeadDim;
+      k_raw[j] = *reinterpret_cast<const float4*>(p);
+      v_raw[j] = *reinterpret_cast<const float4*>(p + a.kv_stride);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      kx[j] = ok[j] ? k_raw[j] : zero;
+      vx[j] = ok[j] ? v_raw[j] : zero;
+    }
+  }
+}
+
+// Folds one loaded chunk into this row's running (m, l, acc).
+__device__ __forceinline__ void consume_chunk(const float4 q4, const float4 (&kx)[4], const float4 (&vx)[4],
+                                              const bool (&ok)[4], float& m, float& l, float4& acc) {
+  float s[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float d = q4.x * kx[j].x;
+    d = fmaf(q4.y, kx[j].y, d);
+    d = fmaf(q4.z, kx[j].z, d);
+    d = fmaf(q4.w, kx[j].w, d);
+    s[j] = row16_sum(d);  // all lanes active here: DPP needs the full row
+  }
+  float mx = m;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (ok[j]) mx = fmaxf(mx, s[j]);
+  if (mx > -INFINITY) {
+    const float corr = __expf(m - mx);  // exp(-inf) = 0 on the row's first valid chunk
+    float ps = 0.f;
+    float4 pv = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float p = ok[j] ? __expf(s[j] - mx) : 0.f;
+      ps += p;
+      pv.x = fmaf(p, vx[j].x, pv.x);
+      pv.y = fmaf(p, vx[j].y, pv.y);
+      pv.z = fmaf(p, vx[j].z, pv.z);
+      pv.w = fmaf(p, vx[j].w, pv.w);
+    }
+    l = fmaf(l, corr, ps);
+    acc.x = fmaf(acc.x, corr, pv.x);
+    acc.y = fmaf(acc.y, corr, pv.y);
+    acc.z = fmaf(acc.z, corr, pv.z);
+    acc.w = fmaf(acc.w, corr, pv.w);
+    m = mx;
+  }
+}
+
+template <int BS_CT>
+__global__ __launch_bounds__(kWave* kHeadsPerGroup) void decode_partition_kernel(const DecodeArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int h = blockIdx.x * kHeadsPerGroup + (threadIdx.x / kWave);
+  const int part = blockIdx.y;
+  const int b = blockIdx.z;
+  if (h >= a.num_heads) return;  // whole wave leaves; the kernel has no barriers
+  const int bs = BS_CT > 0 ? BS_CT : a.block_size;
+  const int ctx = load_context(a, b, part == 0 && h == 0 && lane == 0);
+  float* out_row = a.out + (int64_t)b * a.out_stride + h * kHeadDim;
+  if (ctx == 0) {
+    if (part == 0) out_row[lane] = 0.f;
+    return;
+  }
+  const int t_begin = part * a.part_tokens;
+  if (t_begin >= ctx) return;
+  const int t_end = min(ctx, t_begin + a.part_tokens);
+
+  const int r = lane >> 4;        // DPP row: owns positions t0 + 4j + r
+  const int c = (lane & 15) * 4;  // dims c .. c+3
+  const float4 qraw =
+      *reinterpret_cast<const float4*>(a.q + (int64_t)b * a.q_stride + h * kHeadDim + c);
+  const float4 q4 = make_float4(qraw.x * a.scale, qraw.y * a.scale, qraw.z * a.scale, qraw.w * a.scale);
+  const int32_t* bt = a.block_tables + (int64_t)b * a.bt_stride;
+  const float* head_base = a.pool_layer + (int64_t)h * a.head_stride + c;
+
+  float m = -INFINITY;
+  float l = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+
+  // Two chunks (32 positions) per iteration: all 16 loads are in flight
+  // before the first chunk's math.
+  for (int t0 = t_begin; t0 < t_end; t0 += 2 * kChunk) {
+    float4 ka[4], va[4], kb[4], vb[4];
+    bool oka[4], okb[4];
+    load_chunk<BS_CT>(a, bt, head_base, bs, t0, t_end, r, ka, va, oka);
+    const bool two = t0 + kChunk < t_end;  // uniform across the wave
+    if (two) load_chunk<BS_CT>(a, bt, head_base, bs, t0 + kChunk, t_end, r, kb, vb, okb);
+    consume_chunk(q4, ka, va, oka, m, l, acc);
+    if (two) consume_chunk(q4, kb, vb, okb, m, l, acc);
+  }
+
+  // Merge the four DPP rows (lanes r*16 + i, r = 0..3).
+#pragma unroll
+  for (int sh = 16; sh <= 32; sh *= 2) {
+    const float mo = __shfl_xor(m, sh);
+    const float lo = __shfl_xor(l, sh);
+    float4 ao;
+    ao.x = __shfl_xor(acc.x, sh);
+    ao.y = __shfl_xor(acc.y, sh);
+    ao.z = __shfl_xor(acc.z, sh);
+    ao.w = __shfl_xor(acc.w, sh);
+    const float mn = fmaxf(m, mo);
+    const float ws = m == -INFINITY ? 0.f : __expf(m - mn);
+    const float wo = mo == -INFINITY ? 0.f : __expf(mo - mn);
+    l = l * ws + lo * wo;
+    acc.x = acc.x * ws + ao.x * wo;
+    acc.y = acc.y * ws + ao.y * wo;
+    acc.z = acc.z * ws + ao.z * wo;
+    acc.w = acc.w * ws + ao.w * wo;
+    m = mn;
+  }
+
+  const int nparts = (ctx + a.part_tokens - 1) / a.part_tokens;
+  if (nparts == 1) {
+    if (r == 0) {
+      const float inv = 1.f / l;
+      *reinterpret_cast<float4*>(out_row + c) = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+    }
+  } else {
+    float* pp = a.partials + (((int64_t)b * a.num_heads + h) * a.max_parts + part) * kPartialStride;
+    if (r == 0) *reinterpret_cast<float4*>(pp + c) = acc;
+    if (lane == 0) {
+      pp[kHeadDim] = m;
+      pp[kHeadDim + 1] = l;
+    }
+  }
+}
+
+// Log-sum-exp merge of a sequence's partitions: one wave per (sequence, head), lane = dim.
+__global__ __launch_bounds__(kWave* kHeadsPerGroup) void decode_merge_kernel(const DecodeArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int h = blockIdx.x * kHeadsPerGroup + (threadIdx.x / kWave);
+  const int b = blockIdx.y;
+  if (h >= a.num_heads) return;
+  const int ctx = load_context(a, b, false);
+  const int nparts = (ctx + a.part_tokens - 1) / a.part_tokens;
+  if (nparts <= 1) return;  // written directly by the partition kernel
+  const float* pp = a.partials + ((int64_t)b * a.num_heads + h) * a.max_parts * kPartialStride;
+  float M = -INFINITY;
+  for (int p = 0; p < nparts; ++p) M = fmaxf(M, pp[p * kPartialStride + kHeadDim]);
+  float L = 0.f, O = 0.f;
+  for (int p = 0; p < nparts; ++p) {
+    const float mp = pp[p * kPartialStride + kHeadDim];
+    const float w = mp == -INFINITY ? 0.f : __expf(mp - M);
+    L = fmaf(pp[p * kPartialStride + kHeadDim + 1], w, L);
+    O = fmaf(pp[p * kPartialStride + lane], w, O);
+  }
+  a.out[(int64_t)b * a.out_stride + h * kHeadDim + lane] = O / L;
+}
+
+int choose_partition(int32_t num_seqs, int32_t num_heads, int32_t max_context_len, int32_t requested) {
+  if (requested > 0) return requested;
+  // Enough waves to keep every SIMD of the 256 CUs busy several times over,
+  // without cutting partitions so short that the merge traffic matters.
+  int p = 256;
+  while (p > 32 &&
+         (int64_t)num_seqs * num_heads * ((max_context_len + p - 1) / p) < 8192)
+    p /= 2;
+  return p;
+}
+
+int num_partitions(int32_t max_context_len, int part) {
+  return max_context_len <= 0 ? 1 : (max_context_len + part - 1) / part;
+}
+
+template <int BS_CT>
+void launch_decode(const DecodeArgs& a, int num_seqs, hipStream_t stream) {
+  const dim3 block(kWave * kHeadsPerGroup);
+  const unsigned hgroups = (unsigned)((a.num_heads + kHeadsPerGroup - 1) / kHeadsPerGroup);
+  hipLaunchKernelGGL(decode_partition_kernel<BS_CT>, dim3(hgroups, (unsigned)a.max_parts, (unsigned)num_seqs),
+                     block, 0, stream, a);
+  if (a.max_parts > 1)
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(hgroups, (unsigned)num_seqs), block, 0, stream, a);
+}
+
+}  // namespace
+}  // namespace tq
+
+extern "C" size_t tq_paged_decode_workspace_size(int32_t num_seqs, int32_t num_heads, int32_t head_dim,
+                                                 int32_t max_context_len, int32_t partition_tokens) {
+  using namespace tq;
+  if (num_seqs <= 0 || num_heads <= 0 || head_dim != kHeadDim || max_context_len <= 0) return 0;
+  if (partition_tokens < 0 || partition_tokens % kChunk != 0) return 0;
+  const int part = choose_partition(num_seqs, num_heads, max_context_len, partition_tokens);
+  const int parts = num_partitions(max_context_len, part);
+  if (parts <= 1) return 0;
+  return (size_t)num_seqs * num_heads * parts * kPartialStride * sizeof(float);
+}
+
+extern "C" tq_status tq_paged_decode(float* out, int64_t out_row_stride, const float* q,
+                                     int64_t q_row_stride, const float* pool, int64_t num_blocks,
+                                     int32_t num_layers, int32_t num_heads, int32_t block_size,
+                                     int32_t head_dim, int32_t layer, const int32_t* block_tables,
+                                     int64_t block_table_stride, int32_t max_blocks_per_seq,
+                                     const int32_t* context_lens, int32_t num_seqs,
+                                     int32_t max_context_len, float scale, int32_t partition_tokens,
+                                     void* workspace, size_t workspace_bytes, int32_t* d_error,
+                                     void* stream) {
+  using namespace tq;
+  if (num_seqs < 0 || num_blocks < 1 || num_layers < 1 || num_heads < 1 || block_size < 1 ||
+      head_dim < 1 || layer < 0 || layer >= num_layers || max_blocks_per_seq < 0 ||
+      max_context_len < 0 || partition_tokens < 0 || partition_tokens % kChunk != 0 ||
+      num_blocks > 0x7fffffffLL)
+    return TQ_ERR_INVALID_ARGUMENT;
+  if (head_dim != kHeadDim || block_size > kMaxBlockSize) return TQ_ERR_UNSUPPORTED;
+  if (num_seqs == 0) return TQ_OK;
+  if (out == nullptr || q == nullptr || pool == nullptr || block_tables == nullptr ||
+      context_lens == nullptr)
+    return TQ_ERR_INVALID_ARGUMENT;
+  const int64_t row = (int64_t)num_heads * head_dim;
+  if (out_row_stride < row || q_row_stride < row || block_table_stride < max_blocks_per_seq)
+    return TQ_ERR_INVALID_ARGUMENT;
+  if (((uintptr_t)out | (uintptr_t)q | (uintptr_t)pool) % 16 != 0 || out_row_stride % 4 != 0 ||
+      q_row_stride % 4 != 0)
+    return TQ_ERR_INVALID_ARGUMENT;
+  if (num_seqs > 65535) return TQ_ERR_UNSUPPORTED;
+  if ((int64_t)max_blocks_per_seq * block_size > 0x7fffffffLL) return TQ_ERR_UNSUPPORTED;
+
+  const int part = choose_partition(num_seqs, num_heads, max_context_len, partition_tokens);
+  const int parts = num_partitions(max_context_len, part);
+  if (parts > 65535) return TQ_ERR_UNSUPPORTED;
+  const size_t need = tq_paged_decode_workspace_size(num_seqs, num_heads, head_dim, max_context_len,
+                                                     partition_tokens);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need || (uintptr_t)workspace % 16 != 0))
+    return TQ_ERR_WORKSPACE;
+
+  const PoolGeom g = pool_geom(num_layers, num_heads, block_size, head_dim, layer);
+  DecodeArgs a;
+  a.out = out;
+  a.out_stride = out_row_stride;
+  a.q = q;
+  a.q_stride = q_row_stride;
+  a.pool_layer = pool + g.layer_offset;
+  a.block_stride = g.block_stride;
+  a.kv_stride = g.kv_stride;
+  a.head_stride = g.head_stride;
+  a.block_tables = block_tables;
+  a.bt_stride = block_table_stride;
+  a.context_lens = context_lens;
+  a.partials = static_cast<float*>(workspace);
+  a.d_error = d_error;
+  a.scale = scale;
+  a.num_blocks = (int32_t)num_blocks;
+  a.num_heads = num_heads;
+  a.block_size = block_size;
+  const int64_t cap_blocks = (int64_t)max_blocks_per_seq * block_size;
+  const int64_t cap_grid = (int64_t)parts * part;
+  a.ctx_cap = (int32_t)(cap_blocks < cap_grid ? cap_blocks : cap_grid);
+  a.part_tokens = part;
+  a.max_parts = parts;
+
+  hipStream_t s = (hipStream_t)stream;
+  switch (block_size) {
+    case 16: launch_decode<16>(a, num_seqs, s); break;
+    case 32: launch_decode<32>(a, num_seqs, s); break;
+    default: launch_decode<0>(a, num_seqs, s); break;
+  }
+  return check_launch();
+}

@@ -1,0 +1,273 @@
+// Paged causal prefill / chunked-prefill attention for gfx950 on fp32 MFMA.
+//
+// One 64-lane wave per (16-query tile, head, sequence). Keys are visited in
+// tiles of 16 positions read in place from the block pool. Both products run
+// on v_mfma_f32_16x16x4_f32:
+//
+//   S^T[key][query] = K[key][:] . Q[query][:]        16 MFMAs (K = 64 dims / 4)
+//   O^T[dim][query] += V^T[dim][key] P^T[key][query]  4 steps x 4 dim tiles
+//
+// Computing the transposed score tile S^T keeps the softmax probabilities in
+// the exact lane/register layout the PV product wants as its B operand: lane
+// (j, g) = (lane % 16, lane / 16) holds query j and keys 4g..4g+3 of the tile
+// in S^T's accumulator, and those are the keys step s = 0..3 of the PV product
+// takes from lane group g. No LDS transpose is needed. The A operand of PV is
+// V[key][4i .. 4i+3] for lane i = lane % 16 - one float4 per step that feeds
+// all four dim tiles (dim = 4i + t), so lane (j, g) ends with output dims
+// 16g .. 16g+15 of query j and stores them as four float4.
+//
+// Masking is index arithmetic: query i of sequence b sits at q_start[b] + i
+// and sees keys j <= q_start[b] + i (tokquay/kv_cache.py:208-214). Online
+// softmax keeps one running max per query, shared by its four lane groups.
+//
+// Reference semantics: PagedBatch.gather + mask (tokquay/kv_cache.py:208-214,
+// :234-242) and Attention.forward's masked softmax (tokquay/model.py:94-96).
+
+#include <math.h>
+
+#include "tq_internal.h"
+
+namespace tq {
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTile = 16;  // queries per wave, keys per step
+
+struct PrefillArgs {
+  float* out;
+  int64_t out_stride;
+  const float* q;
+  int64_t q_stride;
+  const float* pool_layer;
+  int64_t block_stride;
+  int64_t kv_stride;
+  int64_t head_stride;
+  const int32_t* block_tables;
+  int64_t bt_stride;
+  const int32_t* cu_q;
+  const int32_t* q_start;
+  int32_t* d_error;
+  float scale;
+  int32_t num_blocks;
+  int32_t num_heads;
+  int32_t block_size;
+  int32_t max_blocks;
+  int32_t num_q_rows;
+};
+
+// Pointer to the first element of position `key` of this head's K tile (V is + kv_stride),
+// or nullptr when the block id is out of range.
+template <int BS_CT>
+__device__ __forceinline__ const float* key_row(const PrefillArgs& a, const int32_t* bt,
+                                                const float* head_base, int bs, int key) {
+  const int bi = BS_CT > 0 ? key / BS_CT : key / bs;
+  const int off = key - bi * (BS_CT > 0 ? BS_CT : bs);
+  const int64_t blk = bt[bi];
+  if ((uint64_t)blk >= (uint64_t)a.num_blocks) {
+    flag_error(a.d_error, TQ_DEVERR_BLOCK_ID);
+    return nullptr;
+  }
+  return head_base + blk * a.block_stride + (int64_t)off * kHeadDim;
+}
+
+template <int BS_CT>
+__global__ __launch_bounds__(kWave) void prefill_kernel(const PrefillArgs a) {
+  const int lane = threadIdx.x;
+  const int qt = blockIdx.x;
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+  const int bs = BS_CT > 0 ? BS_CT : a.block_size;
+
+  const int row0 = a.cu_q[b];
+  const int nq = a.cu_q[b + 1] - row0;
+  const int qi0 = qt * kTile;
+  if (qi0 >= nq) return;
+  const int start = a.q_start[b];
+  if (row0 < 0 || row0 + nq > a.num_q_rows || start < 0 ||
+      (int64_t)start + nq > (int64_t)a.max_blocks * bs) {
+    if (qt == 0 && h == 0 && lane == 0) flag_error(a.d_error, TQ_DEVERR_LENGTH);
+    return;
+  }
+
+  const int j = lane & 15;  // query column of this lane (and dim group i of the PV A operand)
+  const int g = lane >> 4;  // lane group: dims 16g..16g+15 in QK, keys 4g..4g+3 in PV
+  const int qi = qi0 + j;
+  const bool q_ok = qi < nq;
+  const int qpos = start + (q_ok ? qi : nq - 1);  // padded lanes mirror the last real query
+
+  // B operand of the QK product: Q[query j][16g + s], s = 0..15, pre-scaled.
+  float qreg[16];
+  if (q_ok) {
+    const float* qp = a.q + (int64_t)(row0 + qi) * a.q_stride + h * kHeadDim + 16 * g;
+#pragma unroll
+    for (int v4 = 0; v4 < 4; ++v4) {
+      const float4 x = *reinterpret_cast<const float4*>(qp + 4 * v4);
+      qreg[4 * v4 + 0] = x.x * a.scale;
+      qreg[4 * v4 + 1] = x.y * a.scale;
+      qreg[4 * v4 + 2] = x.z * a.scale;
+      qreg[4 * v4 + 3] = x.w * a.scale;
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < 16; ++s) qreg[s] = 0.f;
+  }
+
+  const int32_t* bt = a.block_tables + (int64_t)b * a.bt_stride;
+  const float* head_base = a.pool_layer + (int64_t)h * a.head_stride;
+  const int kend = start + min(qi0 + kTile, nq);  // keys this tile can see: [0, kend)
+
+  floatx4 o[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) o[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY;
+  float l = 0.f;
+
+  for (int kt = 0; kt < kend; kt += kTile) {
+    // A operand of the QK product: K[key kt + j][16g + s].
+    float kreg[16];
+    {
+      const int key = kt + j;
+      const float* p = key < kend ? key_row<BS_CT>(a, bt, head_base, bs, key) : nullptr;
+      if (p != nullptr) {
+        p += 16 * g;
+#pragma unroll
+        for (int v4 = 0; v4 < 4; ++v4) {
+          const float4 x = *reinterpret_cast<const float4*>(p + 4 * v4);
+          kreg[4 * v4 + 0] = x.x;
+          kreg[4 * v4 + 1] = x.y;
+          kreg[4 * v4 + 2] = x.z;
+          kreg[4 * v4 + 3] = x.w;
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < 16; ++s) kreg[s] = 0.f;
+      }
+    }
+    // V rows of the PV A operand: V[key kt + 4g + s][4j .. 4j+3], s = 0..3.
+    float4 vreg[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int key = kt + 4 * g + s;
+      const float* p = key < kend ? key_row<BS_CT>(a, bt, head_base, bs, key) : nullptr;
+      vreg[s] = p != nullptr ? *reinterpret_cast<const float4*>(p + a.kv_stride + 4 * j)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+
+    floatx4 st = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 16; ++s) st = __builtin_amdgcn_mfma_f32_16x16x4f32(kreg[s], qreg[s], st, 0, 0, 0);
+    // st[r] = S^T[key kt + 4g + r][query j]
+
+    float sm[4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int key = kt + 4 * g + r;
+      sm[r] = key <= qpos ? st[r] : -INFINITY;
+      tmax = fmaxf(tmax, sm[r]);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float mn = fmaxf(m, tmax);  // finite: key 0 is visible to every query in tile kt = 0
+    const float corr = __expf(m - mn);
+    float p[4];
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[r] = sm[r] == -INFINITY ? 0.f : __expf(sm[r] - mn);
+      ps += p[r];
+    }
+    l = fmaf(l, corr, ps);
+    m = mn;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) o[t] *= corr;
+
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      o[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(vreg[s].x, p[s], o[0], 0, 0, 0);
+      o[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(vreg[s].y, p[s], o[1], 0, 0, 0);
+      o[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(vreg[s].z, p[s], o[2], 0, 0, 0);
+      o[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vreg[s].w, p[s], o[3], 0, 0, 0);
+    }
+  }
+
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  if (q_ok) {
+    const float inv = 1.f / l;
+    float* op = a.out + (int64_t)(row0 + qi) * a.out_stride + h * kHeadDim + 16 * g;
+    // o[t][r] = O^T[dim-row 4g + r][query j] = output dim 16g + 4r + t.
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      *reinterpret_cast<float4*>(op + 4 * r) =
+          make_float4(o[0][r] * inv, o[1][r] * inv, o[2][r] * inv, o[3][r] * inv);
+  }
+}
+
+template <int BS_CT>
+void launch_prefill(const PrefillArgs& a, int num_seqs, int max_query_len, hipStream_t stream) {
+  const unsigned qtiles = (unsigned)((max_query_len + kTile - 1) / kTile);
+  hipLaunchKernelGGL(prefill_kernel<BS_CT>, dim3(qtiles, (unsigned)a.num_heads, (unsigned)num_seqs),
+                     dim3(kWave), 0, stream, a);
+}
+
+}  // namespace
+}  // namespace tq
+
+extern "C" tq_status tq_paged_prefill(float* out, int64_t out_row_stride, const float* q,
+                                      int64_t q_row_stride, const float* pool, int64_t num_blocks,
+                                      int32_t num_layers, int32_t num_heads, int32_t block_size,
+                                      int32_t head_dim, int32_t layer, const int32_t* block_tables,
+                                      int64_t block_table_stride, int32_t max_blocks_per_seq,
+                                      const int32_t* cu_seqlens_q, const int32_t* q_start,
+                                      int32_t num_seqs, int32_t num_q_rows, int32_t max_query_len,
+                                      float scale, int32_t* d_error, void* stream) {
+  using namespace tq;
+  if (num_seqs < 0 || num_blocks < 1 || num_layers < 1 || num_heads < 1 || block_size < 1 ||
+      head_dim < 1 || layer < 0 || layer >= num_layers || max_blocks_per_seq < 0 ||
+      num_q_rows < 0 || max_query_len < 0 || num_blocks > 0x7fffffffLL)
+    return TQ_ERR_INVALID_ARGUMENT;
+  if (head_dim != kHeadDim || block_size > kMaxBlockSize) return TQ_ERR_UNSUPPORTED;
+  if (num_seqs == 0 || num_q_rows == 0 || max_query_len == 0) return TQ_OK;
+  if (out == nullptr || q == nullptr || pool == nullptr || block_tables == nullptr ||
+      cu_seqlens_q == nullptr || q_start == nullptr)
+    return TQ_ERR_INVALID_ARGUMENT;
+  const int64_t row = (int64_t)num_heads * head_dim;
+  if (out_row_stride < row || q_row_stride < row || block_table_stride < max_blocks_per_seq)
+    return TQ_ERR_INVALID_ARGUMENT;
+  if (((uintptr_t)out | (uintptr_t)q | (uintptr_t)pool) % 16 != 0 || out_row_stride % 4 != 0 ||
+      q_row_stride % 4 != 0)
+    return TQ_ERR_INVALID_ARGUMENT;
+  if (num_seqs > 65535 || num_heads > 65535) return TQ_ERR_UNSUPPORTED;
+  if ((int64_t)max_blocks_per_seq * block_size > 0x7fffffffLL) return TQ_ERR_UNSUPPORTED;
+
+  const PoolGeom g = pool_geom(num_layers, num_heads, block_size, head_dim, layer);
+  PrefillArgs a;
+  a.out = out;
+  a.out_stride = out_row_stride;
+  a.q = q;
+  a.q_stride = q_row_stride;
+  a.pool_layer = pool + g.layer_offset;
+  a.block_stride = g.block_stride;
+  a.kv_stride = g.kv_stride;
+  a.head_stride = g.head_stride;
+  a.block_tables = block_tables;
+  a.bt_stride = block_table_stride;
+  a.cu_q = cu_seqlens_q;
+  a.q_start = q_start;
+  a.d_error = d_error;
+  a.scale = scale;
+  a.num_blocks = (int32_t)num_blocks;
+  a.num_heads = num_heads;
+  a.block_size = block_size;
+  a.max_blocks = max_blocks_per_seq;
+  a.num_q_rows = num_q_rows;
+
+  hipStream_t s = (hipStream_t)stream;
+  switch (block_size) {
+    case 16: launch_prefill<16>(a, num_seqs, max_query_len, s); break;
+    default: launch_prefill<0>(a, num_seqs, max_query_len, s); break;
+  }
+  return check_launch();
+}

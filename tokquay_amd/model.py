@@ -1,0 +1,106 @@
+"""GPT-2 forward over the paged pool, with attention on the gfx950 kernels.
+
+Architecture and parameter names follow the reference's hand-written GPT-2
+(tokquay/model.py:24-181): pre-LN blocks, fused ``c_attn`` QKV projection,
+tanh-approximated GELU, tied LM head, ``nn.Linear`` weights ``[out, in]``.
+
+The paged forward differs in how rows are laid out. The reference runs every
+layer on right-padded ``[B, T, C]`` activations and attends through a gathered
+copy of each sequence's blocks. Here the input ids are packed to the real
+tokens once (``PagedBatch.token_index``), every GEMM / LayerNorm / GELU runs on
+``[N, C]`` with ``N = sum(new_lens)``, and attention is ``PagedBatch.attend``:
+cache write + paged attention read in place from the pool. Padded positions
+are never computed, which is why their logits come back as zeros when
+``last_only`` is False.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from tokquay_amd.kv_cache import PagedBatch
+
+
+@dataclass
+class GPT2Config:
+    vocab_size: int = 50257
+    n_positions: int = 1024
+    n_embd: int = 768
+    n_layer: int = 12
+    n_head: int = 12
+    layer_norm_eps: float = 1e-5
+
+    @property
+    def d_head(self) -> int:
+        return self.n_embd // self.n_head
+
+
+class Attention(nn.Module):
+    def __init__(self, cfg: GPT2Config):
+        super().__init__()
+        self.c_attn = nn.Linear(cfg.n_embd, 3 * cfg.n_embd)
+        self.c_proj = nn.Linear(cfg.n_embd, cfg.n_embd)
+
+    def forward(self, x: torch.Tensor, cache: PagedBatch, layer: int) -> torch.Tensor:
+        # x: [N, C] packed rows. c_attn gives [N, 3C] = [q | k | v], heads contiguous in each.
+        return self.c_proj(cache.attend(layer, self.c_attn(x)))
+
+
+class MLP(nn.Module):
+    def __init__(self, cfg: GPT2Config):
+        super().__init__()
+        self.c_fc = nn.Linear(cfg.n_embd, 4 * cfg.n_embd)
+        self.c_proj = nn.Linear(4 * cfg.n_embd, cfg.n_embd)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.c_proj(F.gelu(self.c_fc(x), approximate="tanh"))
+
+
+class Block(nn.Module):
+    def __init__(self, cfg: GPT2Config):
+        super().__init__()
+        self.ln_1 = nn.LayerNorm(cfg.n_embd, eps=cfg.layer_norm_eps)
+        self.attn = Attention(cfg)
+        self.ln_2 = nn.LayerNorm(cfg.n_embd, eps=cfg.layer_norm_eps)
+        self.mlp = MLP(cfg)
+
+    def forward(self, x: torch.Tensor, cache: PagedBatch, layer: int) -> torch.Tensor:
+        x = x + self.attn(self.ln_1(x), cache, layer)
+        return x + self.mlp(self.ln_2(x))
+
+
+class GPT2(nn.Module):
+    def __init__(self, cfg: GPT2Config | None = None):
+        super().__init__()
+        self.cfg = cfg or GPT2Config()
+        self.wte = nn.Embedding(self.cfg.vocab_size, self.cfg.n_embd)
+        self.wpe = nn.Embedding(self.cfg.n_positions, self.cfg.n_embd)
+        self.h = nn.ModuleList(Block(self.cfg) for _ in range(self.cfg.n_layer))
+        self.ln_f = nn.LayerNorm(self.cfg.n_embd, eps=self.cfg.layer_norm_eps)
+
+    def forward(self, input_ids: torch.Tensor, cache: PagedBatch, last_only: bool = False) -> torch.Tensor:
+        """input_ids ``[B, T]`` (new tokens, right-padded) -> logits ``[B, T, vocab]``, or ``[B, 1, vocab]``
+        of each row's last real token when ``last_only``. Validation follows tokquay/model.py:154-160."""
+        if not isinstance(cache, PagedBatch):
+            raise TypeError("this GPT-2 runs only on the paged pool: pass a PagedBatch")
+        B, T = input_ids.shape
+        if (B, T) != (cache.B, cache.T):
+            raise ValueError(f"input_ids {tuple(input_ids.shape)} does not match batch {(cache.B, cache.T)}")
+        if cache.max_ctx > self.cfg.n_positions:
+            raise ValueError(f"sequence length {cache.max_ctx} exceeds n_positions={self.cfg.n_positions}")
+
+        ids = input_ids.reshape(-1).index_select(0, cache.token_index)  # [N] real tokens only
+        x = self.wte(ids) + self.wpe(cache.packed_positions)  # positions of real tokens are < n_positions
+        for i, block in enumerate(self.h):
+            x = block(x, cache, i)
+        if last_only:
+            x = self.ln_f(x.index_select(0, cache.last_rows))  # [B, C]
+            return (x @ self.wte.weight.T)[:, None]  # tied LM head
+        logits = self.ln_f(x) @ self.wte.weight.T  # [N, vocab]
+        full = logits.new_zeros(B * T, logits.size(-1))
+        full[cache.token_index] = logits
+        return full.view(B, T, -1)

@@ -1,0 +1,174 @@
+"""Tensor-level entry points of the gfx950 paged-attention kernels.
+
+Each function checks its tensors (device, dtype, shapes, inner contiguity),
+then calls the C ABI (``include/tokquay_amd.h``) on torch's current HIP
+stream. Nothing here computes on the host and nothing synchronises.
+
+Shapes (fp32 unless noted; ``H`` heads of ``D = 64`` dims):
+
+* ``pool``: ``[num_blocks, n_layer, 2, H, block_size, D]`` contiguous, the
+  reference's pool layout (tokquay/kv_cache.py:5, :51-53).
+* q / k / v / out rows: ``[N, H, D]`` or ``[N, H*D]``; any row stride, rows
+  contiguous inside (so views of the fused QKV projection output work).
+* ``block_tables``: int32 ``[B, max_blocks]``, rows padded with any valid id.
+* ``slot_mapping``: int64 ``[N]``; -1 marks a padded token that writes nothing.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from tokquay_amd import _lib
+
+HEAD_DIM = 64
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _pool_dims(pool: torch.Tensor) -> tuple[int, int, int, int, int]:
+    if pool.dim() != 6 or pool.size(2) != 2:
+        raise ValueError(f"pool must be [num_blocks, n_layer, 2, n_head, block_size, d_head], got {tuple(pool.shape)}")
+    if pool.dtype != torch.float32 or not pool.is_cuda or not pool.is_contiguous():
+        raise ValueError("pool must be a contiguous float32 tensor on a HIP device")
+    nb, n_layer, _, n_head, bs, d = pool.shape
+    if d != HEAD_DIM:
+        raise ValueError(f"only d_head={HEAD_DIM} is supported, got {d}")
+    return nb, n_layer, n_head, bs, d
+
+
+def _rows(t: torch.Tensor, name: str, n: int, n_head: int, device: torch.device) -> int:
+    """Validates a row tensor and returns its row stride in elements."""
+    if t.dtype != torch.float32 or t.device != device:
+        raise ValueError(f"{name} must be float32 on {device}")
+    if t.size(0) != n:
+        raise ValueError(f"{name} has {t.size(0)} rows, expected {n}")
+    if t.dim() == 3:
+        ok = t.size(1) == n_head and t.size(2) == HEAD_DIM and t.stride(2) == 1 and t.stride(1) == HEAD_DIM
+    elif t.dim() == 2:
+        ok = t.size(1) == n_head * HEAD_DIM and t.stride(1) == 1
+    else:
+        ok = False
+    if not ok:
+        raise ValueError(f"{name} must be [N, {n_head}, {HEAD_DIM}] or [N, {n_head * HEAD_DIM}] with contiguous rows")
+    return t.stride(0) if n > 1 else n_head * HEAD_DIM
+
+
+def _int_tensor(t: torch.Tensor, name: str, dtype: torch.dtype, device: torch.device) -> None:
+    if t.dtype != dtype or t.device != device or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous {dtype} tensor on {device}")
+
+
+def cache_write(
+    pool: torch.Tensor,
+    layer: int,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    d_error: torch.Tensor | None = None,
+) -> None:
+    """Scatter ``k``/``v`` rows into ``pool[:, layer]`` at ``slot_mapping`` (bit-exact copy)."""
+    nb, n_layer, n_head, bs, d = _pool_dims(pool)
+    if not 0 <= layer < n_layer:
+        raise ValueError(f"layer {layer} out of range [0, {n_layer})")
+    n = slot_mapping.numel()
+    _int_tensor(slot_mapping, "slot_mapping", torch.int64, pool.device)
+    ks = _rows(k, "k", n, n_head, pool.device)
+    vs = _rows(v, "v", n, n_head, pool.device)
+    err = d_error.data_ptr() if d_error is not None else None
+    st = _lib.lib().tq_cache_write(
+        pool.data_ptr(), nb, n_layer, n_head, bs, d, layer,
+        k.data_ptr(), ks, v.data_ptr(), vs, slot_mapping.data_ptr(), n, err, _stream(pool.device),
+    )  # fmt: skip
+    _lib.check(st, "tq_cache_write")
+
+
+def decode_workspace_bytes(num_seqs: int, n_head: int, max_context_len: int, partition_tokens: int = 0) -> int:
+    return int(_lib.lib().tq_paged_decode_workspace_size(num_seqs, n_head, HEAD_DIM, max_context_len, partition_tokens))
+
+
+def paged_decode(
+    out: torch.Tensor,
+    q: torch.Tensor,
+    pool: torch.Tensor,
+    layer: int,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    max_context_len: int,
+    scale: float | None = None,
+    partition_tokens: int = 0,
+    workspace: torch.Tensor | None = None,
+    d_error: torch.Tensor | None = None,
+) -> None:
+    """``out[b] = attention(q[b], keys/values 0..context_lens[b]-1 of sequence b)`` read in place."""
+    nb, n_layer, n_head, bs, d = _pool_dims(pool)
+    if not 0 <= layer < n_layer:
+        raise ValueError(f"layer {layer} out of range [0, {n_layer})")
+    n = context_lens.numel()
+    _int_tensor(context_lens, "context_lens", torch.int32, pool.device)
+    if block_tables.dtype != torch.int32 or block_tables.device != pool.device or block_tables.dim() != 2:
+        raise ValueError("block_tables must be an int32 [B, max_blocks] tensor on the pool's device")
+    if block_tables.size(0) != n or (block_tables.size(1) > 1 and block_tables.stride(1) != 1):
+        raise ValueError("block_tables must have one row per sequence with contiguous rows")
+    qs = _rows(q, "q", n, n_head, pool.device)
+    os_ = _rows(out, "out", n, n_head, pool.device)
+    scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
+    need = decode_workspace_bytes(n, n_head, max_context_len, partition_tokens) if n else 0
+    ws_ptr, ws_bytes = None, 0
+    if need:
+        if workspace is None:
+            workspace = torch.empty(need, dtype=torch.uint8, device=pool.device)
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    err = d_error.data_ptr() if d_error is not None else None
+    bt_stride = block_tables.stride(0) if n > 1 else block_tables.size(1)
+    st = _lib.lib().tq_paged_decode(
+        out.data_ptr(), os_, q.data_ptr(), qs, pool.data_ptr(), nb, n_layer, n_head, bs, d, layer,
+        block_tables.data_ptr(), bt_stride, block_tables.size(1),
+        context_lens.data_ptr(), n, int(max_context_len), scale, partition_tokens,
+        ws_ptr, ws_bytes, err, _stream(pool.device),
+    )  # fmt: skip
+    _lib.check(st, "tq_paged_decode")
+
+
+def paged_prefill(
+    out: torch.Tensor,
+    q: torch.Tensor,
+    pool: torch.Tensor,
+    layer: int,
+    block_tables: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    q_start: torch.Tensor,
+    max_query_len: int,
+    scale: float | None = None,
+    d_error: torch.Tensor | None = None,
+) -> None:
+    """Causal attention of each sequence's new rows ``cu_seqlens_q[b]:cu_seqlens_q[b+1]`` (positions
+    ``q_start[b]...``) over its keys ``0 .. q_start[b] + n_b - 1`` read in place from the pool."""
+    nb, n_layer, n_head, bs, d = _pool_dims(pool)
+    if not 0 <= layer < n_layer:
+        raise ValueError(f"layer {layer} out of range [0, {n_layer})")
+    _int_tensor(cu_seqlens_q, "cu_seqlens_q", torch.int32, pool.device)
+    _int_tensor(q_start, "q_start", torch.int32, pool.device)
+    n_seq = q_start.numel()
+    if cu_seqlens_q.numel() != n_seq + 1:
+        raise ValueError("cu_seqlens_q must have num_seqs + 1 entries")
+    if block_tables.dtype != torch.int32 or block_tables.device != pool.device or block_tables.dim() != 2:
+        raise ValueError("block_tables must be an int32 [B, max_blocks] tensor on the pool's device")
+    if block_tables.size(0) != n_seq or (block_tables.size(1) > 1 and block_tables.stride(1) != 1):
+        raise ValueError("block_tables must have one row per sequence with contiguous rows")
+    n_rows = q.size(0)
+    qs = _rows(q, "q", n_rows, n_head, pool.device)
+    os_ = _rows(out, "out", n_rows, n_head, pool.device)
+    scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
+    err = d_error.data_ptr() if d_error is not None else None
+    bt_stride = block_tables.stride(0) if n_seq > 1 else block_tables.size(1)
+    st = _lib.lib().tq_paged_prefill(
+        out.data_ptr(), os_, q.data_ptr(), qs, pool.data_ptr(), nb, n_layer, n_head, bs, d, layer,
+        block_tables.data_ptr(), bt_stride, block_tables.size(1),
+        cu_seqlens_q.data_ptr(), q_start.data_ptr(), n_seq, n_rows, int(max_query_len), scale,
+        err, _stream(pool.device),
+    )  # fmt: skip
+    _lib.check(st, "tq_paged_prefill")
