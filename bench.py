@@ -198,7 +198,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--partition-tokens", type=int, default=0, help="decode partition size (0: automatic)")
     ap.add_argument("--cpu-seqs", type=int, default=256, help="sequences in the CPU baseline sample (0: skip)")
-    ap.add_argument("--cpu-steps", type=int, default=2, help="timed CPU baseline steps (after one warm-up)")
+    ap.add_argument("--cpu-steps", type=int, default=4, help="timed CPU baseline steps (after one warm-up)")
     ap.add_argument("--no-itl", action="store_true", help="skip the 300-request serving trace")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -271,7 +271,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "tq_paged_decode (decode_partition_kernel + decode_merge_kernel)",
+            "kernel": "tq_paged_decode (decode_partition_kernel; decode_merge_kernel when a sequence spans several partitions)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -96,7 +96,7 @@ tq_status tq_cache_write(float* pool, int64_t num_blocks, int32_t num_layers, in
  * max_context_len must be >= every context_lens[b] (it sizes the grid).
  *
  * The kernel splits each sequence into partitions of partition_tokens
- * positions (a multiple of 16; 0 = choose automatically) and merges them with
+ * positions (a multiple of 16, at most 1024; 0 = choose automatically) and merges them with
  * a log-sum-exp pass when a sequence spans several. The merge needs
  * tq_paged_decode_workspace_size(...) bytes of device workspace.
  *

@@ -77,6 +77,9 @@ def test_decode_workspace_size(lib):
     assert lib.tq_paged_decode_workspace_size(64, 12, 64, 200, 256) == 0
     # 256 sequences x 12 heads x 4 partitions of 256 x (64 + 4) floats.
     assert lib.tq_paged_decode_workspace_size(256, 12, 64, 1024, 256) == 256 * 12 * 4 * 68 * 4
-    assert lib.tq_paged_decode_workspace_size(256, 12, 64, 1024, 0) == 256 * 12 * 4 * 68 * 4  # automatic: 256
+    # Automatic: 3072 (sequence, head) pairs already fill the GPU, so one 1024-position partition each.
+    assert lib.tq_paged_decode_workspace_size(256, 12, 64, 1024, 0) == 0
+    assert lib.tq_paged_decode_workspace_size(64, 12, 64, 512, 0) == 64 * 12 * 4 * 68 * 4  # 128-position partitions
     assert lib.tq_paged_decode_workspace_size(4, 12, 64, 1024, 0) == 4 * 12 * 32 * 68 * 4  # small batch: 32
     assert lib.tq_paged_decode_workspace_size(4, 12, 64, 1024, 20) == 0  # invalid partition
+    assert lib.tq_paged_decode_workspace_size(4, 12, 64, 4096, 2048) == 0  # partitions are at most 1024

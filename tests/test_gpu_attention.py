@@ -57,7 +57,7 @@ def test_decode_config2_op(n_layer, layer):
 
 
 @pytest.mark.parametrize("block_size", [1, 4, 8, 16, 32])
-@pytest.mark.parametrize("partition_tokens", [0, 16, 64, 256])
+@pytest.mark.parametrize("partition_tokens", [0, 16, 64, 256, 1024])
 def test_decode_edge_contexts(block_size, partition_tokens):
     ctx = [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 255, 256, 257, 511, 512, 1023, 1024]
     sc = Scenario([c - 1 for c in ctx], [1] * len(ctx), block_size=block_size, seed=block_size)

@@ -3,8 +3,7 @@
 //
 // Decode attention is a GEMV (0.5 flop per byte), so the kernel is built to
 // stream the pool at HBM speed:
-//   * one 64-lane wave per (sequence, head, partition); 4 waves (4 adjacent
-//     heads, whose tiles sit next to each other in the pool) per workgroup;
+//   * one 64-lane wave (one workgroup) per (sequence, head, partition);
 //   * a chunk of 16 positions is read as 4 float4 loads per lane for K and 4
 //     for V. Lane i reads dims 4*(i%16)..+3 of position t0 + 4j + i/16, so
 //     each load instruction covers 1 KiB of a contiguous (block, layer, kv,
@@ -14,7 +13,10 @@
 //   * each DPP row keeps its own running max / sum / accumulator over the
 //     positions it owns, so the loop has no cross-row communication; the four
 //     rows are merged once at the end (xor-16 / xor-32 shuffles);
-//   * the next chunk's 8 loads are issued before the current chunk's math.
+//   * two chunks' 16 loads are issued before the first chunk's math; the
+//     block ids of a partition are fetched once, one per lane, and broadcast
+//     per chunk with v_readlane, so the loop has no table loads;
+//   * K/V loads are non-temporal: every pool element is read once per call.
 // Long contexts are cut into partitions of `part_tokens` positions to fill the
 // 256 CUs; a second small kernel merges the partitions (log-sum-exp).
 //
@@ -30,9 +32,14 @@
 namespace tq {
 namespace {
 
-constexpr int kHeadsPerGroup = 4;               // waves (heads) per workgroup
-constexpr int kChunk = 16;                      // positions per loop iteration
+// Launch shape, chosen by measurement on MI355X (scaled-decode workload): one
+// wave per workgroup and two chunks (16 float4 loads, 16 KiB per wave) in
+// flight per iteration beat 2/4 heads per workgroup and 1/3/4 chunks.
+constexpr int kHeadsPerGroup = 1;  // waves (heads) per workgroup
+constexpr int kChunksPerIter = 2;  // chunks whose loads are issued together
+constexpr int kChunk = 16;         // positions per chunk
 constexpr int kPartialStride = kHeadDim + 4;    // acc[64], m, l, 2 pad: 16-byte aligned rows
+constexpr int kMaxPartition = 1024;             // a partition spans <= 64 blocks of >= 16 positions
 
 struct DecodeArgs {
   float* out;
@@ -66,31 +73,64 @@ __device__ __forceinline__ int load_context(const DecodeArgs& a, int b, bool rep
   return ctx;
 }
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// One 16-byte load of K or V. Each pool element is read exactly once per layer
+// call, so the loads carry the non-temporal hint (measured: 186 -> 165 us per
+// launch on the scaled-decode workload).
+__device__ __forceinline__ float4 load_kv(const float* p) {
+  const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+
+// Per-partition block ids, one per lane, loaded once before the position loop.
+// Lane i holds the id of the partition's i-th block (a partition spans at most
+// 64 blocks), validated against the pool; a chunk then fetches its block id with
+// v_readlane into a scalar register, so the loop issues no table loads at all.
+struct PartitionBlocks {
+  int32_t id;   // this lane's block id (0 when invalid)
+  int32_t ok;   // 1 when the id is inside the pool
+  int first;    // table index of the partition's first block
+};
+
+template <int BS_CT>
+__device__ __forceinline__ PartitionBlocks load_partition_blocks(const DecodeArgs& a, const int32_t* bt,
+                                                                 int t_begin, int t_end, int lane) {
+  PartitionBlocks pb;
+  pb.first = t_begin / BS_CT;
+  const int nblk = (t_end - 1) / BS_CT - pb.first + 1;  // <= 64: part_tokens <= 1024 and BS_CT >= 16
+  pb.id = 0;
+  pb.ok = 0;
+  if (lane < nblk) {
+    const int32_t id = bt[pb.first + lane];
+    pb.ok = (uint32_t)id < (uint32_t)a.num_blocks ? 1 : 0;
+    if (!pb.ok) flag_error(a.d_error, TQ_DEVERR_BLOCK_ID);
+    pb.id = pb.ok ? id : 0;
+  }
+  return pb;
+}
+
 // Loads positions t0 + 4j + r (j = 0..3) of this lane's DPP row r into registers.
 // Branch free: every lane loads from an in-bounds address (positions past
 // t_end re-read a position of the same block, bad block ids read block 0) and
 // invalid positions are zeroed by a select and reported through ok[j].
 template <int BS_CT>
-__device__ __forceinline__ void load_chunk(const DecodeArgs& a, const int32_t* bt,
+__device__ __forceinline__ void load_chunk(const DecodeArgs& a, const int32_t* bt, const PartitionBlocks& pb,
                                            const float* head_base, int bs, int t0, int t_end,
                                            int r, float4 (&kx)[4], float4 (&vx)[4], bool (&ok)[4]) {
   const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
   if constexpr (BS_CT >= kChunk) {
-    // The whole chunk sits in one block (t0 is a multiple of 16 and so is BS_CT),
-    // and t0 < t_end, so bt[t0 / BS_CT] is inside the table row.
-    int64_t blk = bt[t0 / BS_CT];
-    const bool blk_ok = (uint64_t)blk < (uint64_t)a.num_blocks;
-    if (!blk_ok) {
-      if ((threadIdx.x & 63) == 0) flag_error(a.d_error, TQ_DEVERR_BLOCK_ID);
-      blk = 0;
-    }
+    // The whole chunk sits in one block (t0 is a multiple of 16 and so is BS_CT).
+    const int slot = t0 / BS_CT - pb.first;  // wave-uniform
+    const int64_t blk = __builtin_amdgcn_readlane(pb.id, slot);
+    const bool blk_ok = __builtin_amdgcn_readlane(pb.ok, slot) != 0;
     const float* base = head_base + blk * a.block_stride + (int64_t)(t0 % BS_CT) * kHeadDim;
     float4 k_raw[4], v_raw[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float* p = base + (4 * j + r) * kHeadDim;
-      k_raw[j] = *reinterpret_cast<const float4*>(p);
-      v_raw[j] = *reinterpret_cast<const float4*>(p + a.kv_stride);
+      k_raw[j] = load_kv(p);
+      v_raw[j] = load_kv(p + a.kv_stride);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -113,8 +153,8 @@ __device__ __forceinline__ void load_chunk(const DecodeArgs& a, const int32_t* b
       }
       ok[j] = blk_ok && t_req < t_end;
       const float* p = head_base + blk * a.block_stride + (int64_t)(t - bi * bs) * kHeadDim;
-      k_raw[j] = *reinterpret_cast<const float4*>(p);
-      v_raw[j] = *reinterpret_cast<const float4*>(p + a.kv_stride);
+      k_raw[j] = load_kv(p);
+      v_raw[j] = load_kv(p + a.kv_stride);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -192,16 +232,21 @@ __global__ __launch_bounds__(kWave* kHeadsPerGroup) void decode_partition_kernel
   float l = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 
-  // Two chunks (32 positions) per iteration: all 16 loads are in flight
-  // before the first chunk's math.
-  for (int t0 = t_begin; t0 < t_end; t0 += 2 * kChunk) {
-    float4 ka[4], va[4], kb[4], vb[4];
-    bool oka[4], okb[4];
-    load_chunk<BS_CT>(a, bt, head_base, bs, t0, t_end, r, ka, va, oka);
-    const bool two = t0 + kChunk < t_end;  // uniform across the wave
-    if (two) load_chunk<BS_CT>(a, bt, head_base, bs, t0 + kChunk, t_end, r, kb, vb, okb);
-    consume_chunk(q4, ka, va, oka, m, l, acc);
-    if (two) consume_chunk(q4, kb, vb, okb, m, l, acc);
+  PartitionBlocks pb{0, 0, 0};
+  if constexpr (BS_CT >= kChunk) pb = load_partition_blocks<BS_CT>(a, bt, t_begin, t_end, lane);
+
+  // kChunksPerIter chunks per iteration: all their loads are in flight before
+  // the first chunk's math.
+  for (int t0 = t_begin; t0 < t_end; t0 += kChunksPerIter * kChunk) {
+    float4 kx[kChunksPerIter][4], vx[kChunksPerIter][4];
+    bool ok[kChunksPerIter][4];
+#pragma unroll
+    for (int c = 0; c < kChunksPerIter; ++c)
+      if (c == 0 || t0 + c * kChunk < t_end)  // uniform across the wave
+        load_chunk<BS_CT>(a, bt, pb, head_base, bs, t0 + c * kChunk, t_end, r, kx[c], vx[c], ok[c]);
+#pragma unroll
+    for (int c = 0; c < kChunksPerIter; ++c)
+      if (c == 0 || t0 + c * kChunk < t_end) consume_chunk(q4, kx[c], vx[c], ok[c], m, l, acc);
   }
 
   // Merge the four DPP rows (lanes r*16 + i, r = 0..3).
@@ -264,13 +309,11 @@ __global__ __launch_bounds__(kWave* kHeadsPerGroup) void decode_merge_kernel(con
 }
 
 int choose_partition(int32_t num_seqs, int32_t num_heads, int32_t max_context_len, int32_t requested) {
-  if (requested > 0) return requested;
-  // Enough waves to keep every SIMD of the 256 CUs busy several times over,
-  // without cutting partitions so short that the merge traffic matters.
-  int p = 256;
-  while (p > 32 &&
-         (int64_t)num_seqs * num_heads * ((max_context_len + p - 1) / p) < 8192)
-    p /= 2;
+  if (requested > 0) return requested;  // validated: multiple of 16, at most kMaxPartition
+  // The longest partition (fewest merge passes) that still gives about three
+  // waves per SIMD of the 256 CUs; one partition per sequence when it does.
+  int p = kMaxPartition;
+  while (p > 32 && (int64_t)num_seqs * num_heads * ((max_context_len + p - 1) / p) < 3072) p /= 2;
   return p;
 }
 
@@ -295,7 +338,7 @@ extern "C" size_t tq_paged_decode_workspace_size(int32_t num_seqs, int32_t num_h
                                                  int32_t max_context_len, int32_t partition_tokens) {
   using namespace tq;
   if (num_seqs <= 0 || num_heads <= 0 || head_dim != kHeadDim || max_context_len <= 0) return 0;
-  if (partition_tokens < 0 || partition_tokens % kChunk != 0) return 0;
+  if (partition_tokens < 0 || partition_tokens % kChunk != 0 || partition_tokens > kMaxPartition) return 0;
   const int part = choose_partition(num_seqs, num_heads, max_context_len, partition_tokens);
   const int parts = num_partitions(max_context_len, part);
   if (parts <= 1) return 0;
@@ -315,6 +358,7 @@ extern "C" tq_status tq_paged_decode(float* out, int64_t out_row_stride, const f
   if (num_seqs < 0 || num_blocks < 1 || num_layers < 1 || num_heads < 1 || block_size < 1 ||
       head_dim < 1 || layer < 0 || layer >= num_layers || max_blocks_per_seq < 0 ||
       max_context_len < 0 || partition_tokens < 0 || partition_tokens % kChunk != 0 ||
+      partition_tokens > kMaxPartition ||
       num_blocks > 0x7fffffffLL)
     return TQ_ERR_INVALID_ARGUMENT;
   if (head_dim != kHeadDim || block_size > kMaxBlockSize) return TQ_ERR_UNSUPPORTED;
