@@ -49,25 +49,27 @@ def decode_bytes(ctxs: list[int], n_head: int = 12, d: int = 64, bs: int = BLOCK
 
 
 class KernelTimer:
-    """Brackets every tq_paged_decode call of the timed steps with HIP events on the launch stream."""
+    """Times every tq_paged_decode call of the timed steps with HIP events that the launch itself
+    records at the start and end of its kernels (tq_set_decode_timing_events)."""
 
     def __init__(self):
         import torch
 
-        self.torch = torch
+        from tokquay_amd import _lib
+
+        self.torch, self.lib = torch, _lib.lib()
         self.pairs = []
         self.bytes = 0
 
     def __call__(self, batch, phase):
-        if phase == "before":
-            ev = self.torch.cuda.Event(enable_timing=True)
-            ev.record()
-            self.pairs.append([ev, None])
-            self.bytes += decode_bytes([batch.context_lens[b] for b in range(batch.B) if batch.new_lens[b] == 1])
-        else:
-            ev = self.torch.cuda.Event(enable_timing=True)
-            ev.record()
-            self.pairs[-1][1] = ev
+        if phase != "before":
+            return
+        start, stop = self.torch.cuda.Event(enable_timing=True), self.torch.cuda.Event(enable_timing=True)
+        start.record()  # creates the events; the kernel launch records them again at its own start / end
+        stop.record()
+        self.lib.tq_set_decode_timing_events(start.cuda_event, stop.cuda_event)
+        self.pairs.append((start, stop))
+        self.bytes += decode_bytes([batch.context_lens[b] for b in range(batch.B) if batch.new_lens[b] == 1])
 
     def total_ms(self) -> float:
         return sum(a.elapsed_time(b) for a, b in self.pairs)

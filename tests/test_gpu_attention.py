@@ -151,3 +151,24 @@ def test_host_side_argument_errors_raise():
         ops.paged_decode(torch.empty_like(q), q, pool, 0, tables, ctx, 1000, partition_tokens=16, workspace=tiny)
     with pytest.raises(ValueError):
         ops.paged_decode(torch.empty_like(q), q, pool, 1, tables, ctx, 1000)  # layer out of range
+
+
+def test_launch_recorded_timing_events():
+    """tq_set_decode_timing_events: the decode launch records both events around its own kernels."""
+    from tokquay_amd import _lib, ops
+
+    pool = torch.randn(64, 1, 2, 12, 16, 64, device="cuda")
+    q = torch.randn(8, 12, 64, device="cuda")
+    tables = torch.arange(64, dtype=torch.int32, device="cuda").view(8, 8)
+    ctx = torch.full((8,), 128, dtype=torch.int32, device="cuda")
+    want = torch.empty_like(q)
+    ops.paged_decode(want, q, pool, 0, tables, ctx, 128)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    stop.record()
+    assert _lib.lib().tq_set_decode_timing_events(start.cuda_event, stop.cuda_event) == 0
+    got = torch.empty_like(q)
+    ops.paged_decode(got, q, pool, 0, tables, ctx, 128)
+    torch.cuda.synchronize()
+    assert start.elapsed_time(stop) > 0
+    assert torch.equal(got, want)

@@ -52,6 +52,7 @@ SIGNATURES: dict[str, tuple] = {
             c_i32p, ctypes.c_void_p,  # d_error, stream
         ],
     ),
+    "tq_set_decode_timing_events": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
     "tq_paged_decode_workspace_size": (
         ctypes.c_size_t,
         [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32],

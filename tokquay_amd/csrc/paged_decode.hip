@@ -25,6 +25,7 @@
 // (tokquay/model.py:94-96), for a query at position ctx-1 that sees keys
 // 0..ctx-1 (tokquay/kv_cache.py:188, :213-214).
 
+#include <hip/hip_ext.h>
 #include <math.h>
 
 #include "tq_internal.h"
@@ -321,14 +322,21 @@ int num_partitions(int32_t max_context_len, int part) {
   return max_context_len <= 0 ? 1 : (max_context_len + part - 1) / part;
 }
 
+// Timing events armed by tq_set_decode_timing_events for the calling thread's next decode call.
+thread_local hipEvent_t g_timing_start = nullptr;
+thread_local hipEvent_t g_timing_stop = nullptr;
+
 template <int BS_CT>
-void launch_decode(const DecodeArgs& a, int num_seqs, hipStream_t stream) {
+void launch_decode(const DecodeArgs& a, int num_seqs, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   const dim3 block(kWave * kHeadsPerGroup);
   const unsigned hgroups = (unsigned)((a.num_heads + kHeadsPerGroup - 1) / kHeadsPerGroup);
-  hipLaunchKernelGGL(decode_partition_kernel<BS_CT>, dim3(hgroups, (unsigned)a.max_parts, (unsigned)num_seqs),
-                     block, 0, stream, a);
-  if (a.max_parts > 1)
-    hipLaunchKernelGGL(decode_merge_kernel, dim3(hgroups, (unsigned)num_seqs), block, 0, stream, a);
+  const bool merge = a.max_parts > 1;
+  // hipExtLaunchKernelGGL records the events at the dispatch's own start and end
+  // (null events are ignored), so a caller's timing covers exactly these kernels.
+  hipExtLaunchKernelGGL(decode_partition_kernel<BS_CT>, dim3(hgroups, (unsigned)a.max_parts, (unsigned)num_seqs),
+                        block, 0, stream, start, merge ? nullptr : stop, 0, a);
+  if (merge)
+    hipExtLaunchKernelGGL(decode_merge_kernel, dim3(hgroups, (unsigned)num_seqs), block, 0, stream, nullptr, stop, 0, a);
 }
 
 }  // namespace
@@ -355,6 +363,9 @@ extern "C" tq_status tq_paged_decode(float* out, int64_t out_row_stride, const f
                                      void* workspace, size_t workspace_bytes, int32_t* d_error,
                                      void* stream) {
   using namespace tq;
+  // Timing events apply to this call only, whatever it returns.
+  hipEvent_t t_start = g_timing_start, t_stop = g_timing_stop;
+  g_timing_start = g_timing_stop = nullptr;
   if (num_seqs < 0 || num_blocks < 1 || num_layers < 1 || num_heads < 1 || block_size < 1 ||
       head_dim < 1 || layer < 0 || layer >= num_layers || max_blocks_per_seq < 0 ||
       max_context_len < 0 || partition_tokens < 0 || partition_tokens % kChunk != 0 ||
@@ -410,9 +421,15 @@ extern "C" tq_status tq_paged_decode(float* out, int64_t out_row_stride, const f
 
   hipStream_t s = (hipStream_t)stream;
   switch (block_size) {
-    case 16: launch_decode<16>(a, num_seqs, s); break;
-    case 32: launch_decode<32>(a, num_seqs, s); break;
-    default: launch_decode<0>(a, num_seqs, s); break;
+    case 16: launch_decode<16>(a, num_seqs, s, t_start, t_stop); break;
+    case 32: launch_decode<32>(a, num_seqs, s, t_start, t_stop); break;
+    default: launch_decode<0>(a, num_seqs, s, t_start, t_stop); break;
   }
   return check_launch();
+}
+
+extern "C" tq_status tq_set_decode_timing_events(void* start_event, void* stop_event) {
+  tq::g_timing_start = static_cast<hipEvent_t>(start_event);
+  tq::g_timing_stop = static_cast<hipEvent_t>(stop_event);
+  return TQ_OK;
 }
