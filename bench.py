@@ -202,6 +202,9 @@ def main() -> int:
     ap.add_argument("--cpu-seqs", type=int, default=256, help="sequences in the CPU baseline sample (0: skip)")
     ap.add_argument("--cpu-steps", type=int, default=4, help="timed CPU baseline steps (after one warm-up)")
     ap.add_argument("--no-itl", action="store_true", help="skip the 300-request serving trace")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="run 3 copies of a known size (1 GiB read + 1 GiB write) and 3 decode steps, then exit; "
+                    "for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")  # fmt: skip
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path.", file=sys.stderr)
@@ -219,6 +222,18 @@ def main() -> int:
 
     for _ in range(args.warmup):
         engine.step()
+    if args.pmc_probe:
+        x = torch.randn(1 << 28, device="cuda")  # 1 GiB
+        y = torch.empty_like(x)
+        for _ in range(3):
+            torch.neg(x, out=y)  # calibration: reads exactly 1 GiB, writes exactly 1 GiB
+        first_ctx = [s.num_cached_tokens + 1 for s in engine.scheduler.running]  # contexts of the next decode step
+        for _ in range(3):
+            engine.step()
+        torch.cuda.synchronize()
+        print(json.dumps({"pmc_probe": True, "copy_bytes": x.numel() * 4,
+                          "decode_bytes_first_step": decode_bytes(first_ctx)}), flush=True)  # fmt: skip
+        return 0
     running = list(engine.scheduler.running)
     assert len(running) == N_SEQS, f"{len(running)} sequences running, expected {N_SEQS}"
 
