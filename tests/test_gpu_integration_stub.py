@@ -1,0 +1,94 @@
+"""The reference-side binding shown in INTEGRATION.md works: a PagedBatch subclass that calls the
+C ABI through ctypes, plugged into the (restated) reference model's Attention.forward, gives the
+same logits as the reference's own gather path on the same GPU."""
+
+from __future__ import annotations
+
+import math
+import random
+
+import pytest
+import torch
+
+from oracle import gpt2_ref
+from oracle.gpt2_ref import RefConfig, build_ref_model
+from oracle.paged_ref import RefPagedBatch, cdiv, ref_attention
+from tokquay_amd import _lib
+from tokquay_amd.weights import random_state_dict
+
+pytestmark = pytest.mark.gpu
+
+
+class HipRefPagedBatch(RefPagedBatch):
+    """The INTEGRATION.md stub, over the oracle's restatement of the reference PagedBatch."""
+
+    def __init__(self, pool, block_size, block_tables, start, new_lens):
+        super().__init__(pool, block_size, block_tables, start, new_lens)
+        dev, T, bs = pool.device, self.T, block_size
+        idx, slots, cu = [], [], [0]
+        for b, (tbl, s, n) in enumerate(zip(block_tables, start, new_lens)):
+            for t in range(n):
+                idx.append(b * T + t)
+                slots.append(tbl[(s + t) // bs] * bs + (s + t) % bs)
+            cu.append(cu[-1] + n)
+        self.idx = torch.tensor(idx, device=dev)
+        self.slots = torch.tensor(slots, dtype=torch.long, device=dev)
+        self.cu = torch.tensor(cu, dtype=torch.int32, device=dev)
+        self.start_t = torch.tensor(start, dtype=torch.int32, device=dev)
+        self.tables32 = self.block_tables.to(torch.int32)
+        self.max_q = max(new_lens)
+        self.stream = torch.cuda.current_stream().cuda_stream
+
+    def attend(self, layer, q, k, v):
+        L_ = _lib.lib()
+        NB, L, _, H, bs, d = self.pool.shape
+        B, T, N, C = self.B, self.T, self.idx.numel(), H * d
+        pack = lambda t: t.transpose(1, 2).reshape(B * T, C).index_select(0, self.idx)  # noqa: E731
+        q, k, v = pack(q), pack(k), pack(v)
+        out = torch.empty_like(q)
+        _lib.check(L_.tq_cache_write(self.pool.data_ptr(), NB, L, H, bs, d, layer, k.data_ptr(), C,
+                                     v.data_ptr(), C, self.slots.data_ptr(), N, None, self.stream), "write")  # fmt: skip
+        nb = self.tables32.size(1)
+        _lib.check(L_.tq_paged_prefill(out.data_ptr(), C, q.data_ptr(), C, self.pool.data_ptr(), NB, L, H, bs, d,
+                                       layer, self.tables32.data_ptr(), nb, nb, self.cu.data_ptr(),
+                                       self.start_t.data_ptr(), B, N, self.max_q, 1 / math.sqrt(d), None,
+                                       self.stream), "prefill")  # fmt: skip
+        full = out.new_zeros(B * T, C)
+        full[self.idx] = out
+        return full.view(B, T, H, d).transpose(1, 2)
+
+
+def patched_attention_forward(self, x, cache, layer):
+    """The reference Attention.forward with the three-line branch INTEGRATION.md adds."""
+    B, T, C = x.shape
+    q, k, v = self.c_attn(x).split(C, dim=-1)
+    q, k, v = (t.view(B, T, self.n_head, self.d_head).transpose(1, 2) for t in (q, k, v))
+    if hasattr(cache, "attend"):
+        out = cache.attend(layer, q, k, v)
+        return self.c_proj(out.transpose(1, 2).reshape(B, T, C))
+    cache.write(layer, k, v)
+    kk, vv = cache.gather(layer)
+    return self.c_proj(ref_attention(q, kk, vv, cache.mask).transpose(1, 2).reshape(B, T, C))
+
+
+def test_reference_side_binding_matches_the_gather_path(monkeypatch):
+    monkeypatch.setattr(gpt2_ref._Attention, "forward", patched_attention_forward)
+    cfg = RefConfig()
+    model = build_ref_model(cfg, random_state_dict(cfg, seed=0), device="cuda")
+    rng = random.Random(0)
+    bs, starts, lens = 16, [0, 40, 0, 100], [30, 1, 7, 1]
+    tables, nxt = [], 0
+    for s, n in zip(starts, lens):
+        k = cdiv(s + n, bs)
+        tables.append(list(range(nxt, nxt + k)))
+        nxt += k
+    pool = torch.randn(nxt + 2, cfg.n_layer, 2, cfg.n_head, bs, cfg.d_head, device="cuda")  # history = noise
+    ids = torch.tensor([[rng.randrange(50256) for _ in range(max(lens))] for _ in lens], device="cuda")
+    outs = []
+    for cls in (RefPagedBatch, HipRefPagedBatch):
+        p = pool.clone()
+        with torch.no_grad():
+            outs.append(model(ids, cls(p, bs, tables, starts, lens), last_only=True)[:, 0])
+        outs.append(p)
+    torch.testing.assert_close(outs[2], outs[0], rtol=1e-3, atol=1e-3)  # logits
+    assert torch.equal(outs[3], outs[1])  # identical pools after the step
