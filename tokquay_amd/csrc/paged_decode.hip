@@ -331,12 +331,18 @@ void launch_decode(const DecodeArgs& a, int num_seqs, hipStream_t stream, hipEve
   const dim3 block(kWave * kHeadsPerGroup);
   const unsigned hgroups = (unsigned)((a.num_heads + kHeadsPerGroup - 1) / kHeadsPerGroup);
   const bool merge = a.max_parts > 1;
-  // hipExtLaunchKernelGGL records the events at the dispatch's own start and end
-  // (null events are ignored), so a caller's timing covers exactly these kernels.
-  hipExtLaunchKernelGGL(decode_partition_kernel<BS_CT>, dim3(hgroups, (unsigned)a.max_parts, (unsigned)num_seqs),
-                        block, 0, stream, start, merge ? nullptr : stop, 0, a);
-  if (merge)
-    hipExtLaunchKernelGGL(decode_merge_kernel, dim3(hgroups, (unsigned)num_seqs), block, 0, stream, nullptr, stop, 0, a);
+  const dim3 part_grid(hgroups, (unsigned)a.max_parts, (unsigned)num_seqs);
+  const dim3 merge_grid(hgroups, (unsigned)num_seqs);
+  if (start == nullptr && stop == nullptr) {
+    // The plain launch (what a HIP graph captures).
+    hipLaunchKernelGGL(decode_partition_kernel<BS_CT>, part_grid, block, 0, stream, a);
+    if (merge) hipLaunchKernelGGL(decode_merge_kernel, merge_grid, block, 0, stream, a);
+    return;
+  }
+  // hipExtLaunchKernelGGL records the events at the dispatch's own start and end,
+  // so a caller's timing covers exactly these kernels.
+  hipExtLaunchKernelGGL(decode_partition_kernel<BS_CT>, part_grid, block, 0, stream, start, merge ? nullptr : stop, 0, a);
+  if (merge) hipExtLaunchKernelGGL(decode_merge_kernel, merge_grid, block, 0, stream, nullptr, stop, 0, a);
 }
 
 }  // namespace

@@ -12,6 +12,7 @@ from dataclasses import dataclass
 import torch
 
 from tokquay_amd.generate import paged_forward
+from tokquay_amd.graphs import DecodeGraphs
 from tokquay_amd.kv_cache import BlockAllocator
 from tokquay_amd.model import GPT2
 from tokquay_amd.scheduler import Scheduler, SchedulerConfig
@@ -83,7 +84,10 @@ class Engine:
         allocator: BlockAllocator,
         config: SchedulerConfig | None = None,
         eos_token_id: int = GPT2_EOS_TOKEN_ID,
+        use_graphs: bool | None = None,
     ):
+        """``use_graphs`` (default: on when the pool is on a HIP device) replays decode steps
+        from captured HIP graphs; prefill and mixed steps always run eagerly."""
         if config is None:
             config = SchedulerConfig(max_model_len=model.cfg.n_positions)
         if config.max_model_len > model.cfg.n_positions:
@@ -96,6 +100,9 @@ class Engine:
         self.last_step: StepInfo | None = None
         self._next_id = 0
         self._rngs: dict[int, torch.Generator] = {}
+        if use_graphs is None:
+            use_graphs = allocator.pool.is_cuda
+        self.graphs = DecodeGraphs(model, allocator, config.max_num_seqs) if use_graphs else None
 
     def add_request(self, prompt_token_ids: list[int], params: SamplingParams | None = None) -> Sequence:
         seq = Sequence(self._next_id, list(prompt_token_ids), sampling=params or SamplingParams())
@@ -139,7 +146,10 @@ class Engine:
         st.positions_computed += sum(s.num_uncached_tokens for s in batch.seqs)
         st.positions_padded += batch.padded_tokens
 
-        logits = paged_forward(self.model, self.allocator, batch.seqs)
+        if self.graphs is not None and not batch.is_prefill:
+            logits = self.graphs.forward(batch.seqs)
+        else:
+            logits = paged_forward(self.model, self.allocator, batch.seqs)
         self.last_step = StepInfo(batch.is_prefill, len(batch.seqs), batch.padded_tokens, self.kv_snapshot())
         tokens = self._sample(batch.seqs, logits)
 

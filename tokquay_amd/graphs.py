@@ -1,0 +1,178 @@
+"""HIP-graph replay of decode steps.
+
+A decode step (every sequence feeds one token) runs ~180 small launches from
+Python; at 256 sequences that host work is a third of the step. This module
+captures the whole decode forward (embeddings, 12 layers with the cache-write
+and paged-decode kernels, LM head) once per batch bucket (powers of two) into a
+HIP graph and replays it.
+
+What changes between steps lives in static device buffers at fixed addresses,
+refreshed by one host-to-device copy per step: token ids, positions, slots,
+block tables (``n_positions / block_size`` columns, padded with block 0) and
+context lengths. The decode kernel's grid is sized for ``n_positions`` and its
+waves skip partitions past each sequence's real context, so one graph serves
+every context length. Rows past the live batch are padding: slot -1 (the cache
+write skips them) and context 0 (the decode kernel writes zeros); their logits
+are ignored.
+
+No memset, host synchronisation or allocation happens inside the captured
+region except torch's own graph-pool allocations.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from tokquay_amd import _lib
+from tokquay_amd.kv_cache import HEAD_DIM, BlockAllocator, cdiv
+from tokquay_amd.sequence import Sequence
+
+
+def bucket_for(n: int) -> int:
+    return 1 << max(0, (n - 1).bit_length())
+
+
+class StaticDecodeBatch:
+    """Fixed-address decode metadata for up to ``capacity`` sequences."""
+
+    def __init__(self, allocator: BlockAllocator, capacity: int, n_positions: int):
+        pool = allocator.pool
+        if not pool.is_cuda or pool.dtype != torch.float32 or pool.shape[-1] != HEAD_DIM:
+            raise ValueError("graph decode needs a float32 pool with d_head=64 on a HIP device")
+        self.allocator, self.pool, self.capacity = allocator, pool, capacity
+        self.block_size = allocator.block_size
+        self.max_ctx = n_positions
+        self.max_blocks = cdiv(n_positions, self.block_size)
+        dev = pool.device
+        cap, mb = capacity, self.max_blocks
+        self.d64 = torch.zeros(3 * cap, dtype=torch.int64, device=dev)  # ids | positions | slots
+        self.d32 = torch.zeros(cap * mb + cap, dtype=torch.int32, device=dev)  # tables | context lengths
+        self.h64 = torch.zeros(3 * cap, dtype=torch.int64, pin_memory=True)
+        self.h32 = torch.zeros(cap * mb + cap, dtype=torch.int32, pin_memory=True)
+        self.copied = torch.cuda.Event()
+        self.ids, self.positions, self.slots = self.d64[:cap], self.d64[cap : 2 * cap], self.d64[2 * cap :]
+        self.tables = self.d32[: cap * mb].view(cap, mb)
+        self.context_lens = self.d32[cap * mb :]
+        n_head = pool.shape[3]
+        L = _lib.lib()
+        ws = max(int(L.tq_paged_decode_workspace_size(b, n_head, HEAD_DIM, n_positions, 0))
+                 for b in self.buckets())  # fmt: skip
+        self.workspace = torch.empty(max(ws, 16), dtype=torch.uint8, device=dev)
+        self.error_word = allocator.error_word
+
+    def buckets(self) -> list[int]:
+        out, b = [], 1
+        while b <= self.capacity:
+            out.append(b)
+            b *= 2
+        return out
+
+    def fill(self, seqs: list[Sequence], bucket: int) -> None:
+        """Write this step's metadata for ``seqs`` (each feeding its one uncached token) and pad to ``bucket``."""
+        self.copied.synchronize()  # the previous step's copy has left the staging buffers
+        cap, mb, bs = self.capacity, self.max_blocks, self.block_size
+        a64 = self.h64.numpy()
+        a32 = self.h32.numpy()
+        ids, pos, slots = a64[:cap], a64[cap : 2 * cap], a64[2 * cap :]
+        tables = a32[: cap * mb].reshape(cap, mb)
+        ctx = a32[cap * mb :]
+        n = len(seqs)
+        for i, s in enumerate(seqs):
+            p = s.num_cached_tokens
+            if s.num_tokens - p != 1:
+                raise ValueError("graph decode steps feed exactly one token per sequence")
+            ids[i] = s.token_ids[p]
+            pos[i] = p
+            tbl = s.block_table
+            slots[i] = tbl[p // bs] * bs + p % bs
+            k = cdiv(p + 1, bs)
+            tables[i, :k] = tbl[:k]
+            tables[i, k:] = 0
+            ctx[i] = p + 1
+        ids[n:bucket] = 0
+        pos[n:bucket] = 0
+        slots[n:bucket] = -1
+        tables[n:bucket] = 0
+        ctx[n:bucket] = 0
+        self.d64.copy_(self.h64, non_blocking=True)
+        self.d32.copy_(self.h32, non_blocking=True)
+        self.copied.record()
+
+    def view(self, bucket: int) -> "StaticDecodeView":
+        return StaticDecodeView(self, bucket)
+
+
+class StaticDecodeView:
+    """``attend(layer, qkv)`` over the first ``rows`` rows of a StaticDecodeBatch (the graph's batch)."""
+
+    def __init__(self, static: StaticDecodeBatch, rows: int):
+        self.s, self.rows = static, rows
+
+    def attend(self, layer: int, qkv: torch.Tensor) -> torch.Tensor:
+        s, n = self.s, self.rows
+        pool = s.pool
+        nb, n_layer, _, n_head, bs, d = pool.shape
+        C = n_head * d
+        L = _lib.lib()
+        out = torch.empty(n, C, dtype=torch.float32, device=pool.device)
+        stream = torch.cuda.current_stream(pool.device).cuda_stream
+        err = s.error_word.data_ptr() if s.error_word is not None else None
+        qp, pp = qkv.data_ptr(), pool.data_ptr()
+        _lib.check(L.tq_cache_write(pp, nb, n_layer, n_head, bs, d, layer, qp + 4 * C, 3 * C, qp + 8 * C, 3 * C,
+                                    s.slots.data_ptr(), n, err, stream), "tq_cache_write")  # fmt: skip
+        _lib.check(
+            L.tq_paged_decode(out.data_ptr(), C, qp, 3 * C, pp, nb, n_layer, n_head, bs, d, layer,
+                              s.tables.data_ptr(), s.max_blocks, s.max_blocks, s.context_lens.data_ptr(), n,
+                              s.max_ctx, 1.0 / math.sqrt(d), 0, s.workspace.data_ptr(), s.workspace.numel(),
+                              err, stream),
+            "tq_paged_decode",
+        )  # fmt: skip
+        return out
+
+
+class DecodeGraphs:
+    """Captured decode forwards, one per batch bucket, sharing one StaticDecodeBatch."""
+
+    def __init__(self, model, allocator: BlockAllocator, max_batch: int):
+        self.model = model
+        self.static = StaticDecodeBatch(allocator, bucket_for(max_batch), model.cfg.n_positions)
+        self.graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
+
+    def _forward(self, rows: int) -> torch.Tensor:
+        m, s = self.model, self.static
+        view = s.view(rows)
+        x = m.wte(s.ids[:rows]) + m.wpe(s.positions[:rows])
+        for i, block in enumerate(m.h):
+            x = block(x, view, i)
+        return m.ln_f(x) @ m.wte.weight.T
+
+    def _capture(self, rows: int) -> None:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):  # warm-up launches (same inputs: the K/V writes are idempotent)
+            for _ in range(2):
+                self._forward(rows)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            logits = self._forward(rows)
+        self.graphs[rows] = (graph, logits)
+
+    @torch.no_grad()
+    def forward(self, seqs: list[Sequence]) -> torch.Tensor:
+        """Logits ``[len(seqs), vocab]`` of one decode step; advances ``num_cached_tokens``."""
+        rows = bucket_for(len(seqs))
+        if rows > self.static.capacity:
+            raise ValueError(f"{len(seqs)} sequences exceed the graph capacity {self.static.capacity}")
+        self.static.fill(seqs, rows)
+        if rows not in self.graphs:
+            self._capture(rows)
+        graph, logits = self.graphs[rows]
+        graph.replay()
+        for s in seqs:
+            s.num_cached_tokens += 1
+        return logits[: len(seqs)]
+
+
