@@ -91,4 +91,7 @@ def test_reference_side_binding_matches_the_gather_path(monkeypatch):
             outs.append(model(ids, cls(p, bs, tables, starts, lens), last_only=True)[:, 0])
         outs.append(p)
     torch.testing.assert_close(outs[2], outs[0], rtol=1e-3, atol=1e-3)  # logits
-    assert torch.equal(outs[3], outs[1])  # identical pools after the step
+    # Layer 0's K/V come straight from the embeddings: written bit-identically. Deeper layers' K/V
+    # depend on earlier attention outputs, which agree to fp32 rounding.
+    assert torch.equal(outs[3][:, 0], outs[1][:, 0])
+    torch.testing.assert_close(outs[3], outs[1], rtol=1e-4, atol=1e-4)
