@@ -23,6 +23,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import torch
 
 from tokquay_amd import _lib
@@ -61,6 +62,7 @@ class StaticDecodeBatch:
                  for b in self.buckets())  # fmt: skip
         self.workspace = torch.empty(max(ws, 16), dtype=torch.uint8, device=dev)
         self.error_word = allocator.error_word
+        self._rows: dict[int, tuple[np.ndarray, int]] = {}  # seq_id -> (padded table row, table length)
 
     def buckets(self) -> list[int]:
         out, b = [], 1
@@ -73,29 +75,38 @@ class StaticDecodeBatch:
         """Write this step's metadata for ``seqs`` (each feeding its one uncached token) and pad to ``bucket``."""
         self.copied.synchronize()  # the previous step's copy has left the staging buffers
         cap, mb, bs = self.capacity, self.max_blocks, self.block_size
+        n = len(seqs)
         a64 = self.h64.numpy()
         a32 = self.h32.numpy()
-        ids, pos, slots = a64[:cap], a64[cap : 2 * cap], a64[2 * cap :]
         tables = a32[: cap * mb].reshape(cap, mb)
-        ctx = a32[cap * mb :]
-        n = len(seqs)
+        # Block-table rows: a host mirror per live sequence, refreshed only when its table grew.
+        live = {}
         for i, s in enumerate(seqs):
             p = s.num_cached_tokens
             if s.num_tokens - p != 1:
                 raise ValueError("graph decode steps feed exactly one token per sequence")
-            ids[i] = s.token_ids[p]
-            pos[i] = p
+            row, known = self._rows.get(s.seq_id, (None, -1))
             tbl = s.block_table
-            slots[i] = tbl[p // bs] * bs + p % bs
-            k = cdiv(p + 1, bs)
-            tables[i, :k] = tbl[:k]
-            tables[i, k:] = 0
-            ctx[i] = p + 1
-        ids[n:bucket] = 0
-        pos[n:bucket] = 0
-        slots[n:bucket] = -1
+            if row is None or known != len(tbl) or row[0] != tbl[0]:
+                row = np.zeros(mb, dtype=np.int32)
+                k = min(len(tbl), mb)
+                row[:k] = tbl[:k]
+                known = len(tbl)
+            live[s.seq_id] = (row, known)
+            tables[i] = row
+        self._rows = live
+        pos = np.fromiter((s.num_cached_tokens for s in seqs), dtype=np.int64, count=n)
+        last = np.fromiter(((s.output_token_ids or s.prompt_token_ids)[-1] for s in seqs), dtype=np.int64, count=n)
+        blk = tables[np.arange(n), pos // bs].astype(np.int64)
+        a64[:n] = last  # the token at position num_cached_tokens is the sequence's last one
+        a64[cap : cap + n] = pos
+        a64[2 * cap : 2 * cap + n] = blk * bs + pos % bs
+        a32[cap * mb : cap * mb + n] = pos + 1
+        a64[n:bucket] = 0
+        a64[cap + n : cap + bucket] = 0
+        a64[2 * cap + n : 2 * cap + bucket] = -1  # padded rows write nothing
         tables[n:bucket] = 0
-        ctx[n:bucket] = 0
+        a32[cap * mb + n : cap * mb + bucket] = 0  # and attend to nothing
         self.d64.copy_(self.h64, non_blocking=True)
         self.d32.copy_(self.h32, non_blocking=True)
         self.copied.record()
