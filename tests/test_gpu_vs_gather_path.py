@@ -41,7 +41,7 @@ def test_hip_engine_beats_the_reference_gather_path():
     engine = Engine(model, alloc, SchedulerConfig(max_num_seqs=N, max_num_batched_tokens=32768))
     rng = random.Random(7)
     for _ in range(N):
-        ctx = rng.randint(256, 1024 - 2 * STEPS - 4)
+        ctx = rng.randint(256, 1024 - 4 * STEPS)
         engine.add_request([rng.randrange(50256) for _ in range(ctx)], SamplingParams(max_tokens=4 * STEPS, ignore_eos=True))
     while engine.scheduler.waiting:
         engine.step()
