@@ -55,7 +55,7 @@ def decode_bytes(ctxs: list[int], n_head: int = 12, d: int = 64, bs: int = BLOCK
 
 class KernelTimer:
     """Times every tq_paged_decode call of the timed steps with HIP events that the launch itself
-    records at the start and end of its kernels (tq_set_decode_timing_events)."""
+    records at the start and end of its kernels (tq_set_timing_events)."""
 
     def __init__(self):
         import torch
@@ -72,7 +72,7 @@ class KernelTimer:
         start, stop = self.torch.cuda.Event(enable_timing=True), self.torch.cuda.Event(enable_timing=True)
         start.record()  # creates the events; the kernel launch records them again at its own start / end
         stop.record()
-        self.lib.tq_set_decode_timing_events(start.cuda_event, stop.cuda_event)
+        self.lib.tq_set_timing_events(start.cuda_event, stop.cuda_event)
         self.pairs.append((start, stop))
         self.bytes += decode_bytes([batch.context_lens[b] for b in range(batch.B) if batch.new_lens[b] == 1])
 

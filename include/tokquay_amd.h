@@ -66,6 +66,16 @@ int32_t tq_abi_version(void);
 const char* tq_last_hip_error(void);
 
 /*
+ * Arms two hipEvent_t handles (passed as void*; either may be NULL) for the
+ * calling thread's next tq_paged_decode or tq_paged_prefill call: the start
+ * event is recorded when that call's first kernel starts and the stop event
+ * when its last kernel ends, so hipEventElapsedTime gives the kernels' own
+ * duration, without launch gaps. That call disarms them, whatever it returns.
+ * No counterpart in the reference (it has no kernels); for benchmarks.
+ */
+tq_status tq_set_timing_events(void* start_event, void* stop_event);
+
+/*
  * Cache write: for every token n in [0, num_tokens) with slot = slot_mapping[n] >= 0,
  *   pool[slot / block_size][layer][0][h][slot % block_size][:] = k[n * k_row_stride + h * 64 + :]
  *   pool[slot / block_size][layer][1][h][slot % block_size][:] = v[n * v_row_stride + h * 64 + :]
@@ -114,16 +124,6 @@ tq_status tq_paged_decode(float* out, int64_t out_row_stride,
                           float scale, int32_t partition_tokens,
                           void* workspace, size_t workspace_bytes,
                           int32_t* d_error, void* stream);
-
-/*
- * Arms two hipEvent_t handles (passed as void*; either may be NULL) for the
- * calling thread's next tq_paged_decode call: the start event is recorded when
- * its first kernel starts and the stop event when its last kernel ends, so
- * hipEventElapsedTime gives the kernels' own duration, without launch gaps.
- * The next tq_paged_decode call disarms them, whatever it returns.
- * No counterpart in the reference (it has no kernels); for benchmarks.
- */
-tq_status tq_set_decode_timing_events(void* start_event, void* stop_event);
 
 /* Bytes of workspace tq_paged_decode needs for these sizes (0 if none). */
 size_t tq_paged_decode_workspace_size(int32_t num_seqs, int32_t num_heads, int32_t head_dim,

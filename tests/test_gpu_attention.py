@@ -154,7 +154,7 @@ def test_host_side_argument_errors_raise():
 
 
 def test_launch_recorded_timing_events():
-    """tq_set_decode_timing_events: the decode launch records both events around its own kernels."""
+    """tq_set_timing_events: the decode launch records both events around its own kernels."""
     from tokquay_amd import _lib, ops
 
     pool = torch.randn(64, 1, 2, 12, 16, 64, device="cuda")
@@ -166,9 +166,20 @@ def test_launch_recorded_timing_events():
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     stop.record()
-    assert _lib.lib().tq_set_decode_timing_events(start.cuda_event, stop.cuda_event) == 0
+    assert _lib.lib().tq_set_timing_events(start.cuda_event, stop.cuda_event) == 0
     got = torch.empty_like(q)
     ops.paged_decode(got, q, pool, 0, tables, ctx, 128)
     torch.cuda.synchronize()
     assert start.elapsed_time(stop) > 0
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("num_seqs", [24, 12, 6, 2])  # 4608 / 2304 / 1152 / 384 query tiles: key split 1 / 2 / 4 / 8
+def test_prefill_key_split_widths(num_seqs):
+    """The prefill launch splits each query tile's keys over 1, 2, 4 or 8 waves depending on how many
+    tiles there are; every width must match the reference, with ragged lengths and chunk starts."""
+    rng = random.Random(num_seqs)
+    lens = [256] + [rng.randint(100, 256) for _ in range(num_seqs - 1)]
+    starts = [rng.choice([0, 0, 100, 300]) for _ in range(num_seqs)]
+    sc = Scenario(starts, lens, block_size=16, seed=90 + num_seqs)
+    check(sc, brute=num_seqs <= 6)

@@ -27,6 +27,7 @@ SIGNATURES: dict[str, tuple] = {
     "tq_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "tq_abi_version": (ctypes.c_int32, []),
     "tq_last_hip_error": (ctypes.c_char_p, []),
+    "tq_set_timing_events": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
     "tq_cache_write": (
         ctypes.c_int,
         [
@@ -52,7 +53,6 @@ SIGNATURES: dict[str, tuple] = {
             c_i32p, ctypes.c_void_p,  # d_error, stream
         ],
     ),
-    "tq_set_decode_timing_events": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
     "tq_paged_decode_workspace_size": (
         ctypes.c_size_t,
         [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32],

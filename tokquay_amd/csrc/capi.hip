@@ -6,6 +6,8 @@
 
 namespace {
 thread_local char g_last_hip_error[256] = "";
+thread_local hipEvent_t g_timing_start = nullptr;
+thread_local hipEvent_t g_timing_stop = nullptr;
 }
 
 namespace tq {
@@ -15,7 +17,19 @@ tq_status record_hip_error(hipError_t err) {
   g_last_hip_error[sizeof(g_last_hip_error) - 1] = '\0';
   return TQ_ERR_HIP;
 }
+
+TimingEvents take_timing_events() {
+  TimingEvents t{g_timing_start, g_timing_stop};
+  g_timing_start = g_timing_stop = nullptr;
+  return t;
+}
 }  // namespace tq
+
+extern "C" tq_status tq_set_timing_events(void* start_event, void* stop_event) {
+  g_timing_start = static_cast<hipEvent_t>(start_event);
+  g_timing_stop = static_cast<hipEvent_t>(stop_event);
+  return TQ_OK;
+}
 
 extern "C" const char* tq_status_string(tq_status status) {
   switch (status) {

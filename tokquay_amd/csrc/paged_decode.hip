@@ -322,10 +322,6 @@ int num_partitions(int32_t max_context_len, int part) {
   return max_context_len <= 0 ? 1 : (max_context_len + part - 1) / part;
 }
 
-// Timing events armed by tq_set_decode_timing_events for the calling thread's next decode call.
-thread_local hipEvent_t g_timing_start = nullptr;
-thread_local hipEvent_t g_timing_stop = nullptr;
-
 template <int BS_CT>
 void launch_decode(const DecodeArgs& a, int num_seqs, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   const dim3 block(kWave * kHeadsPerGroup);
@@ -370,8 +366,8 @@ extern "C" tq_status tq_paged_decode(float* out, int64_t out_row_stride, const f
                                      void* stream) {
   using namespace tq;
   // Timing events apply to this call only, whatever it returns.
-  hipEvent_t t_start = g_timing_start, t_stop = g_timing_stop;
-  g_timing_start = g_timing_stop = nullptr;
+  const TimingEvents timing = take_timing_events();
+  hipEvent_t t_start = timing.start, t_stop = timing.stop;
   if (num_seqs < 0 || num_blocks < 1 || num_layers < 1 || num_heads < 1 || block_size < 1 ||
       head_dim < 1 || layer < 0 || layer >= num_layers || max_blocks_per_seq < 0 ||
       max_context_len < 0 || partition_tokens < 0 || partition_tokens % kChunk != 0 ||
@@ -434,8 +430,3 @@ extern "C" tq_status tq_paged_decode(float* out, int64_t out_row_stride, const f
   return check_launch();
 }
 
-extern "C" tq_status tq_set_decode_timing_events(void* start_event, void* stop_event) {
-  tq::g_timing_start = static_cast<hipEvent_t>(start_event);
-  tq::g_timing_stop = static_cast<hipEvent_t>(stop_event);
-  return TQ_OK;
-}

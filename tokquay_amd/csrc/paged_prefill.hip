@@ -1,8 +1,10 @@
 // Paged causal prefill / chunked-prefill attention for gfx950 on fp32 MFMA.
 //
-// One 64-lane wave per (16-query tile, head, sequence). Keys are visited in
-// tiles of 16 positions read in place from the block pool. Both products run
-// on v_mfma_f32_16x16x4_f32:
+// One workgroup per (16-query tile, head, sequence); its KS waves split the
+// tile's keys (wave w takes key tiles w, w + KS, ...) and merge their partial
+// softmax states through LDS at the end, so a launch with few tiles still
+// fills the GPU. Keys are visited in tiles of 16 positions read in place from
+// the block pool. Both products run on v_mfma_f32_16x16x4_f32:
 //
 //   S^T[key][query] = K[key][:] . Q[query][:]        16 MFMAs (K = 64 dims / 4)
 //   O^T[dim][query] += V^T[dim][key] P^T[key][query]  4 steps x 4 dim tiles
@@ -23,6 +25,7 @@
 // Reference semantics: PagedBatch.gather + mask (tokquay/kv_cache.py:208-214,
 // :234-242) and Attention.forward's masked softmax (tokquay/model.py:94-96).
 
+#include <hip/hip_ext.h>
 #include <math.h>
 
 #include "tq_internal.h"
@@ -54,7 +57,28 @@ struct PrefillArgs {
   int32_t block_size;
   int32_t max_blocks;
   int32_t num_q_rows;
+  int32_t qtiles;     // query tiles per (sequence, head): ceil(max_query_len / 16)
+  int32_t num_seqs;
+  int32_t total;      // qtiles * num_heads * num_seqs workgroups
 };
+
+constexpr int kXcds = 8;  // MI355X: workgroup i is dispatched to XCD i % 8
+
+// Maps the dispatch index to a work tile so that the XCD that runs dispatches
+// x, x+8, x+16, ... gets one contiguous run of tiles: all query tiles of a
+// (sequence, head) land on one XCD and share its L2 for their K/V reads. Inside
+// a (sequence, head), the last query tiles (the most keys, under the causal
+// mask) are dispatched first.
+__device__ __forceinline__ void tile_of(const PrefillArgs& a, int& qt, int& h, int& b) {
+  const int p = blockIdx.x;
+  const int per = a.total / kXcds, rem = a.total % kXcds;
+  const int xcd = p % kXcds, local = p / kXcds;
+  const int l = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+  const int seq_head = l / a.qtiles;
+  qt = a.qtiles - 1 - (l - seq_head * a.qtiles);
+  h = seq_head % a.num_heads;
+  b = seq_head / a.num_heads;
+}
 
 // Pointer to the first element of position `key` of this head's K tile (V is + kv_stride),
 // or nullptr when the block id is out of range.
@@ -72,11 +96,40 @@ __device__ __forceinline__ const float* key_row(const PrefillArgs& a, const int3
 }
 
 template <int BS_CT>
-__global__ __launch_bounds__(kWave) void prefill_kernel(const PrefillArgs a) {
-  const int lane = threadIdx.x;
-  const int qt = blockIdx.x;
-  const int h = blockIdx.y;
-  const int b = blockIdx.z;
+__device__ __forceinline__ void load_kv_tile(const PrefillArgs& a, const int32_t* bt, const float* head_base, int bs,
+                                             int kt, int kend, int j, int g, float (&kreg)[16], float4 (&vreg)[4]) {
+  {
+    const int key = kt + j;
+    const float* p = key < kend ? key_row<BS_CT>(a, bt, head_base, bs, key) : nullptr;
+    if (p != nullptr) {
+      p += 16 * g;
+#pragma unroll
+      for (int v4 = 0; v4 < 4; ++v4) {
+        const float4 x = *reinterpret_cast<const float4*>(p + 4 * v4);
+        kreg[4 * v4 + 0] = x.x;
+        kreg[4 * v4 + 1] = x.y;
+        kreg[4 * v4 + 2] = x.z;
+        kreg[4 * v4 + 3] = x.w;
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < 16; ++s) kreg[s] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int key = kt + 4 * g + s;
+    const float* p = key < kend ? key_row<BS_CT>(a, bt, head_base, bs, key) : nullptr;
+    vreg[s] = p != nullptr ? *reinterpret_cast<const float4*>(p + a.kv_stride + 4 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+
+template <int BS_CT, int KS>
+__global__ __launch_bounds__(kWave* KS) void prefill_kernel(const PrefillArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  int qt, h, b;
+  tile_of(a, qt, h, b);
   const int bs = BS_CT > 0 ? BS_CT : a.block_size;
 
   const int row0 = a.cu_q[b];
@@ -123,37 +176,12 @@ __global__ __launch_bounds__(kWave) void prefill_kernel(const PrefillArgs a) {
   float m = -INFINITY;
   float l = 0.f;
 
-  for (int kt = 0; kt < kend; kt += kTile) {
-    // A operand of the QK product: K[key kt + j][16g + s].
+  // Wave w of the workgroup visits key tiles w, w + KS, w + 2 KS, ...: the QK A
+  // operand K[kt + j][16g + s] and the PV A operand rows V[kt + 4g + s][4j .. 4j+3].
+  for (int kt = wave * kTile; kt < kend; kt += KS * kTile) {
     float kreg[16];
-    {
-      const int key = kt + j;
-      const float* p = key < kend ? key_row<BS_CT>(a, bt, head_base, bs, key) : nullptr;
-      if (p != nullptr) {
-        p += 16 * g;
-#pragma unroll
-        for (int v4 = 0; v4 < 4; ++v4) {
-          const float4 x = *reinterpret_cast<const float4*>(p + 4 * v4);
-          kreg[4 * v4 + 0] = x.x;
-          kreg[4 * v4 + 1] = x.y;
-          kreg[4 * v4 + 2] = x.z;
-          kreg[4 * v4 + 3] = x.w;
-        }
-      } else {
-#pragma unroll
-        for (int s = 0; s < 16; ++s) kreg[s] = 0.f;
-      }
-    }
-    // V rows of the PV A operand: V[key kt + 4g + s][4j .. 4j+3], s = 0..3.
     float4 vreg[4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int key = kt + 4 * g + s;
-      const float* p = key < kend ? key_row<BS_CT>(a, bt, head_base, bs, key) : nullptr;
-      vreg[s] = p != nullptr ? *reinterpret_cast<const float4*>(p + a.kv_stride + 4 * j)
-                             : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-
+    load_kv_tile<BS_CT>(a, bt, head_base, bs, kt, kend, j, g, kreg, vreg);
     floatx4 st = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 16; ++s) st = __builtin_amdgcn_mfma_f32_16x16x4f32(kreg[s], qreg[s], st, 0, 0, 0);
@@ -169,13 +197,17 @@ __global__ __launch_bounds__(kWave) void prefill_kernel(const PrefillArgs a) {
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float mn = fmaxf(m, tmax);  // finite: key 0 is visible to every query in tile kt = 0
-    const float corr = __expf(m - mn);
+    const float mn = fmaxf(m, tmax);
+    // A wave whose tiles start past a query's position has seen no visible key
+    // for it yet (mn = -inf): any finite reference keeps its state exactly zero
+    // (corr = exp(-inf) = 0, every p = 0) without a divergent branch.
+    const float mref = mn == -INFINITY ? 0.f : mn;
+    const float corr = __expf(m - mref);
     float p[4];
     float ps = 0.f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      p[r] = sm[r] == -INFINITY ? 0.f : __expf(sm[r] - mn);
+      p[r] = sm[r] == -INFINITY ? 0.f : __expf(sm[r] - mref);
       ps += p[r];
     }
     l = fmaf(l, corr, ps);
@@ -194,22 +226,82 @@ __global__ __launch_bounds__(kWave) void prefill_kernel(const PrefillArgs a) {
 
   l += __shfl_xor(l, 16);
   l += __shfl_xor(l, 32);
-  if (q_ok) {
-    const float inv = 1.f / l;
-    float* op = a.out + (int64_t)(row0 + qi) * a.out_stride + h * kHeadDim + 16 * g;
-    // o[t][r] = O^T[dim-row 4g + r][query j] = output dim 16g + 4r + t.
+  if constexpr (KS == 1) {
+    if (q_ok) {
+      const float inv = 1.f / l;
+      float* op = a.out + (int64_t)(row0 + qi) * a.out_stride + h * kHeadDim + 16 * g;
+      // o[t][r] = O^T[dim-row 4g + r][query j] = output dim 16g + 4r + t.
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        *reinterpret_cast<float4*>(op + 4 * r) =
+            make_float4(o[0][r] * inv, o[1][r] * inv, o[2][r] * inv, o[3][r] * inv);
+    }
+  } else {
+    // Merge the KS partial states (m, l, O) per query through LDS. Lane (j, g) of
+    // wave w stores its 16 output dims 16g .. 16g+15 in order; lanes of group 0
+    // store the query's m and l (equal across groups).
+    __shared__ float s_o[KS][kWave][16];
+    __shared__ float s_ml[KS][2][kTile];
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      *reinterpret_cast<float4*>(op + 4 * r) =
-          make_float4(o[0][r] * inv, o[1][r] * inv, o[2][r] * inv, o[3][r] * inv);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) s_o[wave][lane][4 * r + t] = o[t][r];
+    if (g == 0) {
+      s_ml[wave][0][j] = m;
+      s_ml[wave][1][j] = l;
+    }
+    __syncthreads();
+    // Thread (wave w, lane) finishes dims 16g + 4w' .. +3 of query j for w' = w, w + KS, ... < 4.
+    for (int part = wave; part < 4; part += KS) {
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < KS; ++w) M = fmaxf(M, s_ml[w][0][j]);
+      float L = 0.f;
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int w = 0; w < KS; ++w) {
+        const float mw = s_ml[w][0][j];
+        const float cw = mw == -INFINITY ? 0.f : __expf(mw - M);  // waves that saw no key weigh 0
+        L = fmaf(s_ml[w][1][j], cw, L);
+        acc.x = fmaf(s_o[w][lane][4 * part + 0], cw, acc.x);
+        acc.y = fmaf(s_o[w][lane][4 * part + 1], cw, acc.y);
+        acc.z = fmaf(s_o[w][lane][4 * part + 2], cw, acc.z);
+        acc.w = fmaf(s_o[w][lane][4 * part + 3], cw, acc.w);
+      }
+      if (q_ok) {
+        const float inv = 1.f / L;
+        float* op = a.out + (int64_t)(row0 + qi) * a.out_stride + h * kHeadDim + 16 * g + 4 * part;
+        *reinterpret_cast<float4*>(op) = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+      }
+    }
   }
 }
 
+template <int BS_CT, int KS>
+void launch_prefill_ks(const PrefillArgs& a, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+  if (start == nullptr && stop == nullptr)
+    hipLaunchKernelGGL((prefill_kernel<BS_CT, KS>), dim3((unsigned)a.total), dim3(kWave * KS), 0, stream, a);
+  else
+    hipExtLaunchKernelGGL((prefill_kernel<BS_CT, KS>), dim3((unsigned)a.total), dim3(kWave * KS), 0, stream, start,
+                          stop, 0, a);
+}
+
+// Waves per workgroup: enough (sequence, head, query tile) work items times KS
+// to give every SIMD of the 256 CUs about four waves.
+int choose_key_split(int64_t tiles) {
+  int ks = 1;
+  while (ks < 8 && tiles * ks < 4096) ks *= 2;
+  return ks;
+}
+
 template <int BS_CT>
-void launch_prefill(const PrefillArgs& a, int num_seqs, int max_query_len, hipStream_t stream) {
-  const unsigned qtiles = (unsigned)((max_query_len + kTile - 1) / kTile);
-  hipLaunchKernelGGL(prefill_kernel<BS_CT>, dim3(qtiles, (unsigned)a.num_heads, (unsigned)num_seqs),
-                     dim3(kWave), 0, stream, a);
+void launch_prefill(const PrefillArgs& a, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+  switch (choose_key_split(a.total)) {
+    case 1: launch_prefill_ks<BS_CT, 1>(a, stream, start, stop); break;
+    case 2: launch_prefill_ks<BS_CT, 2>(a, stream, start, stop); break;
+    case 4: launch_prefill_ks<BS_CT, 4>(a, stream, start, stop); break;
+    default: launch_prefill_ks<BS_CT, 8>(a, stream, start, stop); break;
+  }
 }
 
 }  // namespace
@@ -224,6 +316,7 @@ extern "C" tq_status tq_paged_prefill(float* out, int64_t out_row_stride, const 
                                       int32_t num_seqs, int32_t num_q_rows, int32_t max_query_len,
                                       float scale, int32_t* d_error, void* stream) {
   using namespace tq;
+  const TimingEvents timing = take_timing_events();  // for this call only, whatever it returns
   if (num_seqs < 0 || num_blocks < 1 || num_layers < 1 || num_heads < 1 || block_size < 1 ||
       head_dim < 1 || layer < 0 || layer >= num_layers || max_blocks_per_seq < 0 ||
       num_q_rows < 0 || max_query_len < 0 || num_blocks > 0x7fffffffLL)
@@ -239,7 +332,8 @@ extern "C" tq_status tq_paged_prefill(float* out, int64_t out_row_stride, const 
   if (((uintptr_t)out | (uintptr_t)q | (uintptr_t)pool) % 16 != 0 || out_row_stride % 4 != 0 ||
       q_row_stride % 4 != 0)
     return TQ_ERR_INVALID_ARGUMENT;
-  if (num_seqs > 65535 || num_heads > 65535) return TQ_ERR_UNSUPPORTED;
+  const int64_t qtiles = ((int64_t)max_query_len + kTile - 1) / kTile;
+  if (qtiles * num_heads * num_seqs > 0x7fffffffLL) return TQ_ERR_UNSUPPORTED;
   if ((int64_t)max_blocks_per_seq * block_size > 0x7fffffffLL) return TQ_ERR_UNSUPPORTED;
 
   const PoolGeom g = pool_geom(num_layers, num_heads, block_size, head_dim, layer);
@@ -263,11 +357,14 @@ extern "C" tq_status tq_paged_prefill(float* out, int64_t out_row_stride, const 
   a.block_size = block_size;
   a.max_blocks = max_blocks_per_seq;
   a.num_q_rows = num_q_rows;
+  a.qtiles = (int32_t)qtiles;
+  a.num_seqs = num_seqs;
+  a.total = (int32_t)(qtiles * num_heads * num_seqs);
 
   hipStream_t s = (hipStream_t)stream;
   switch (block_size) {
-    case 16: launch_prefill<16>(a, num_seqs, max_query_len, s); break;
-    default: launch_prefill<0>(a, num_seqs, max_query_len, s); break;
+    case 16: launch_prefill<16>(a, s, timing.start, timing.stop); break;
+    default: launch_prefill<0>(a, s, timing.start, timing.stop); break;
   }
   return check_launch();
 }

@@ -33,6 +33,14 @@ inline PoolGeom pool_geom(int32_t num_layers, int32_t num_heads, int32_t block_s
 // Records `err` as the calling thread's last HIP error message and returns TQ_ERR_HIP.
 tq_status record_hip_error(hipError_t err);
 
+// Timing events armed by tq_set_timing_events for the calling thread's next
+// decode or prefill call; taking them disarms them.
+struct TimingEvents {
+  hipEvent_t start;
+  hipEvent_t stop;
+};
+TimingEvents take_timing_events();
+
 // Checks the launch that was just enqueued.
 inline tq_status check_launch() {
   hipError_t e = hipGetLastError();
