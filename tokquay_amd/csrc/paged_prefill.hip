@@ -124,6 +124,30 @@ __device__ __forceinline__ void load_kv_tile(const PrefillArgs& a, const int32_t
   }
 }
 
+// Same loads when a 16-key tile is exactly one block (block size 16): the tile's
+// block id arrives as a wave-uniform scalar (blk < 0: out of range, load zeros).
+__device__ __forceinline__ void load_kv_block_tile(const PrefillArgs& a, const float* head_base, int64_t blk,
+                                                   int kt, int kend, int j, int g, float (&kreg)[16],
+                                                   float4 (&vreg)[4]) {
+  const float* base = head_base + (blk < 0 ? 0 : blk) * a.block_stride;
+  const bool k_ok = blk >= 0 && kt + j < kend;
+  const float* kp = base + j * kHeadDim + 16 * g;
+#pragma unroll
+  for (int v4 = 0; v4 < 4; ++v4) {
+    const float4 x = k_ok ? *reinterpret_cast<const float4*>(kp + 4 * v4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    kreg[4 * v4 + 0] = x.x;
+    kreg[4 * v4 + 1] = x.y;
+    kreg[4 * v4 + 2] = x.z;
+    kreg[4 * v4 + 3] = x.w;
+  }
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const bool v_ok = blk >= 0 && kt + 4 * g + s < kend;
+    vreg[s] = v_ok ? *reinterpret_cast<const float4*>(base + a.kv_stride + (4 * g + s) * kHeadDim + 4 * j)
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+
 template <int BS_CT, int KS>
 __global__ __launch_bounds__(kWave* KS) void prefill_kernel(const PrefillArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -178,10 +202,31 @@ __global__ __launch_bounds__(kWave* KS) void prefill_kernel(const PrefillArgs a)
 
   // Wave w of the workgroup visits key tiles w, w + KS, w + 2 KS, ...: the QK A
   // operand K[kt + j][16g + s] and the PV A operand rows V[kt + 4g + s][4j .. 4j+3].
+  // Block size 16: tile i is block table entry i. The ids of 64 consecutive tiles
+  // are held one per lane and fetched per tile with v_readlane (no table loads in
+  // the loop); the lane copy is refreshed when the wave moves to the next 64.
+  int tb_base = -1;
+  int32_t tb_id = 0;
   for (int kt = wave * kTile; kt < kend; kt += KS * kTile) {
     float kreg[16];
     float4 vreg[4];
-    load_kv_tile<BS_CT>(a, bt, head_base, bs, kt, kend, j, g, kreg, vreg);
+    if constexpr (BS_CT == kTile) {
+      const int ti = kt / kTile;
+      if ((ti & ~63) != tb_base) {  // wave-uniform
+        tb_base = ti & ~63;
+        const int nblk = (kend + kTile - 1) / kTile;
+        tb_id = -1;
+        if (tb_base + lane < nblk) {
+          const int32_t id = bt[tb_base + lane];
+          if ((uint32_t)id < (uint32_t)a.num_blocks) tb_id = id;
+          else flag_error(a.d_error, TQ_DEVERR_BLOCK_ID);
+        }
+      }
+      const int64_t blk = __builtin_amdgcn_readlane(tb_id, ti - tb_base);
+      load_kv_block_tile(a, head_base, blk, kt, kend, j, g, kreg, vreg);
+    } else {
+      load_kv_tile<BS_CT>(a, bt, head_base, bs, kt, kend, j, g, kreg, vreg);
+    }
     floatx4 st = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 16; ++s) st = __builtin_amdgcn_mfma_f32_16x16x4f32(kreg[s], qreg[s], st, 0, 0, 0);
