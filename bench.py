@@ -32,6 +32,7 @@ if ROOT not in sys.path:
 
 METRIC = "decode tok/s (1 GPU); paged-attn HBM GB/s as % of peak; p50 ITL"
 HBM_PEAK_GBS = 8000.0
+MFMA_FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix
 N_SEQS, CTX_LO, CTX_HI, BLOCK, POOL_BLOCKS = 256, 256, 1024, 16, 16384
 # HBM bytes the decode kernel moves per algorithmic byte on this workload, from two rocprofv3
 # counter runs on ``bench.py --pmc-probe`` (FETCH_SIZE scaled x2.0 and WRITE_SIZE x1.0, the factors
@@ -53,31 +54,41 @@ def decode_bytes(ctxs: list[int], n_head: int = 12, d: int = 64, bs: int = BLOCK
     return kv + qo + meta
 
 
-class KernelTimer:
-    """Times every tq_paged_decode call of the timed steps with HIP events that the launch itself
-    records at the start and end of its kernels (tq_set_timing_events)."""
+class LaunchTimer:
+    """Times every attention launch of one kind ("decode" or "prefill") with HIP events that the
+    launch itself records at the start and end of its kernels (tq_set_timing_events)."""
 
-    def __init__(self):
+    def __init__(self, kind: str):
         import torch
 
         from tokquay_amd import _lib
 
-        self.torch, self.lib = torch, _lib.lib()
+        self.torch, self.lib, self.kind = torch, _lib.lib(), kind
         self.pairs = []
         self.bytes = 0
+        self.flops = 0
 
-    def __call__(self, batch, phase):
-        if phase != "before":
+    def __call__(self, batch, kind):
+        if kind != self.kind:
             return
         start, stop = self.torch.cuda.Event(enable_timing=True), self.torch.cuda.Event(enable_timing=True)
         start.record()  # creates the events; the kernel launch records them again at its own start / end
         stop.record()
         self.lib.tq_set_timing_events(start.cuda_event, stop.cuda_event)
         self.pairs.append((start, stop))
-        self.bytes += decode_bytes([batch.context_lens[b] for b in range(batch.B) if batch.new_lens[b] == 1])
+        rows = [b for b in range(batch.B) if (batch.new_lens[b] == 1) == (kind == "decode")]
+        if kind == "decode":
+            self.bytes += decode_bytes([batch.context_lens[b] for b in rows])
+        else:
+            self.flops += prefill_flops([batch.start[b] for b in rows], [batch.new_lens[b] for b in rows])
 
     def total_ms(self) -> float:
         return sum(a.elapsed_time(b) for a, b in self.pairs)
+
+
+def prefill_flops(starts: list[int], lens: list[int], n_head: int = 12, d: int = 64) -> int:
+    """Causal-exact flops of one prefill layer call: QK^T and PV over the visible keys only."""
+    return sum(4 * n_head * d * (n * s + n * (n + 1) // 2) for s, n in zip(starts, lens))
 
 
 def build_engine(steps_needed: int, seed: int = 0):
@@ -198,6 +209,73 @@ def itl_trace(seed: int = 0, rate: float = 8.0, n: int = 300):
     }
 
 
+def mixed_chunked_step(seed: int = 5) -> dict:
+    """Mixed chunked-prefill + decode steps: 4 prompts of U[512,1024] random tokens fed in 256-token
+    chunks (chunk k starts at 256k) next to 128 sequences decoding at context U[64,768], block size 16.
+    Reports the prefill kernel's MFMA utilisation (causal-exact flops / launch time / fp32 peak)."""
+    import torch
+
+    from tokquay_amd import kv_cache
+    from tokquay_amd.generate import paged_forward
+    from tokquay_amd.kv_cache import BlockAllocator
+    from tokquay_amd.model import GPT2, GPT2Config
+    from tokquay_amd.sequence import Sequence
+    from tokquay_amd.weights import random_state_dict
+
+    cfg = GPT2Config()
+    model = GPT2(cfg)
+    model.load_state_dict(random_state_dict(cfg, seed=0))
+    model = model.cuda().eval()
+    alloc = BlockAllocator(cfg, 8192, BLOCK, device="cuda")
+    rng = random.Random(seed)
+    prompts = [Sequence(i, [rng.randrange(50256) for _ in range(rng.randint(512, 1024))]) for i in range(4)]
+    decoders = [Sequence(4 + i, [rng.randrange(50256) for _ in range(rng.randint(64, 768) - 1)]) for i in range(128)]
+    for s in prompts + decoders:
+        alloc.allocate(s)
+    for i in range(0, 128, 32):  # prefill the decoding sequences' contexts (untimed)
+        nxt = paged_forward(model, alloc, decoders[i : i + 32]).argmax(-1).tolist()
+        for s, t in zip(decoders[i : i + 32], nxt):
+            s.append_token(t)
+            alloc.append_slot(s)
+    chunks = []
+    for k in range(4):
+        live = [p for p in prompts if p.num_cached_tokens < p.num_tokens]
+        seqs = live + decoders
+        lens = [min(256, p.num_tokens - p.num_cached_tokens) for p in live] + [1] * len(decoders)
+        starts = [p.num_cached_tokens for p in live]
+        timer = LaunchTimer("prefill")
+        kv_cache.PagedBatch.launch_hook = timer
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        nxt = paged_forward(model, alloc, seqs, lens).argmax(-1).tolist()
+        torch.cuda.synchronize()
+        step_ms = (time.perf_counter() - t0) * 1e3
+        kv_cache.PagedBatch.launch_hook = None
+        for s, t in zip(decoders, nxt[len(live) :]):
+            s.append_token(t)
+            alloc.append_slot(s)
+        if not timer.pairs:
+            continue
+        us = timer.total_ms() / len(timer.pairs) * 1e3
+        flops = timer.flops / len(timer.pairs)
+        chunks.append({"chunk": k, "prompt_rows": len(live), "starts": starts, "prefill_us": round(us, 2),
+                       "mflop_per_launch": round(flops / 1e6, 1), "tflops": round(flops / us / 1e6, 2),
+                       "frac": round(flops / us / 1e6 / MFMA_FP32_PEAK_TFLOPS, 4), "step_ms": round(step_ms, 3)})  # fmt: skip
+    alloc.check_device_errors()
+    tot_f = sum(c["mflop_per_launch"] for c in chunks)
+    tot_us = sum(c["prefill_us"] for c in chunks)
+    return {
+        "workload": "4 prompts U[512,1024] in 256-token chunks + 128 decoding sequences, ctx U[64,768], block 16",
+        "kernel": "tq_paged_prefill (fp32 MFMA 16x16x4)",
+        "bound": "mfma",
+        "achieved": round(tot_f / tot_us, 2),
+        "peak": MFMA_FP32_PEAK_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(tot_f / tot_us / MFMA_FP32_PEAK_TFLOPS, 4),
+        "chunks": chunks,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -207,6 +285,7 @@ def main() -> int:
     ap.add_argument("--cpu-seqs", type=int, default=256, help="sequences in the CPU baseline sample (0: skip)")
     ap.add_argument("--cpu-steps", type=int, default=4, help="timed CPU baseline steps (after one warm-up)")
     ap.add_argument("--no-itl", action="store_true", help="skip the 300-request serving trace")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the mixed chunked-prefill measurement")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="run 3 copies of a known size (1 GiB read + 1 GiB write) and 3 decode steps, then exit; "
                     "for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")  # fmt: skip
@@ -264,15 +343,15 @@ def main() -> int:
     # Kernel timing: K more decode steps run eagerly, every decode launch timed by HIP events
     # the launch itself records at the start and end of its kernels.
     graphs, engine.graphs = engine.graphs, None
-    timer = KernelTimer()
-    kv_cache.PagedBatch.decode_hook = timer
+    timer = LaunchTimer("decode")
+    kv_cache.PagedBatch.launch_hook = timer
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     for _ in range(args.steps):
         engine.step()
     torch.cuda.synchronize()
     eager_ms = (time.perf_counter() - t1) * 1e3 / args.steps
-    kv_cache.PagedBatch.decode_hook = None
+    kv_cache.PagedBatch.launch_hook = None
     engine.graphs = graphs
     engine.allocator.check_device_errors()
     n_launch = len(timer.pairs)
@@ -339,6 +418,12 @@ def main() -> int:
             "greedy_ids_match_gpu": match,
         }
         del cpu_pool
+    del engine, graphs
+    torch.cuda.empty_cache()
+    if not args.no_prefill:
+        log("mixed chunked-prefill + decode steps ...")
+        result["prefill"] = mixed_chunked_step()
+        log(f"prefill: {result['prefill']['achieved']} TFLOP/s = {result['prefill']['frac']:.3f} of fp32 MFMA peak")
     if not args.no_itl:
         log("serving trace: 300 requests, Poisson 8 req/s ...")
         result["itl"] = itl_trace()

@@ -183,9 +183,9 @@ class PagedBatch(BatchedKV):
     flat ``[B * T]`` padded input, ``last_rows`` gives each sequence's last row.
     """
 
-    # Optional callable(batch, "before" | "after") run around every decode-attention launch
-    # (a benchmark brackets the launch with HIP events on the same stream).
-    decode_hook = None
+    # Optional callable(batch, kind) run right before every decode ("decode") and prefill
+    # ("prefill") attention launch; a benchmark uses it to arm launch-recorded timing events.
+    launch_hook = None
 
     def __init__(
         self,
@@ -370,9 +370,8 @@ class PagedBatch(BatchedKV):
             if self._workspace is None:
                 self._ws_bytes = int(L.tq_paged_decode_workspace_size(Bd, n_head, d, self.decode_max_ctx, self.partition_tokens))
                 self._workspace = torch.empty(max(self._ws_bytes, 1), dtype=torch.uint8, device=pool.device)
-            hook = PagedBatch.decode_hook
-            if hook is not None:
-                hook(self, "before")
+            if PagedBatch.launch_hook is not None:
+                PagedBatch.launch_hook(self, "decode")
             _lib.check(
                 L.tq_paged_decode(op, C, qp, row3, pp, nb, n_layer, n_head, bs, d, layer,
                                   self.decode_block_tables.data_ptr(), self._nbd, self._nbd,
@@ -380,9 +379,9 @@ class PagedBatch(BatchedKV):
                                   self.partition_tokens, self._workspace.data_ptr(), self._ws_bytes, err, stream),
                 "tq_paged_decode",
             )  # fmt: skip
-            if hook is not None:
-                hook(self, "after")
         if self.num_prefill:
+            if PagedBatch.launch_hook is not None:
+                PagedBatch.launch_hook(self, "prefill")
             _lib.check(
                 L.tq_paged_prefill(op + 4 * Bd * C, C, qp + 4 * Bd * row3, row3, pp, nb, n_layer, n_head, bs, d, layer,
                                    self.prefill_block_tables.data_ptr(), self._nbp, self._nbp,
