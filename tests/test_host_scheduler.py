@@ -225,3 +225,101 @@ def test_random_workloads_never_deadlock_or_leak(workload, num_blocks, block_siz
             assert len(s.block_table) >= cdiv(s.num_cached_tokens, block_size)
     assert all(s.status is SequenceStatus.FINISHED and len(s.output_token_ids) == s.sampling.max_tokens for s in accepted)
     assert alloc.num_free_blocks == alloc.num_blocks
+
+
+# ------------------------------------------------------------------- chunked prefill (mixed steps)
+def fake_step_chunked(sched):
+    """The forward consumed new_lens[i] tokens of each sequence; complete ones append a token."""
+    batch = sched.schedule()
+    if batch is None:
+        return None
+    for s, n in zip(batch.seqs, batch.new_lens):
+        s.num_cached_tokens += n
+        if s.num_cached_tokens == s.num_tokens:
+            s.append_token(0)
+            if len(s.output_token_ids) >= s.sampling.max_tokens:
+                sched.finish(s, "length")
+    return batch
+
+
+def test_chunked_prompt_is_fed_next_to_decoding_sequences_without_stalling_them():
+    sched = make(num_blocks=64, block_size=4, max_num_batched_tokens=40, max_num_seqs=8, chunked_prefill=True, prefill_chunk_tokens=32)
+    a = req(sched, 0, 6, 30)
+    fake_step_chunked(sched)  # A prefills (6 tokens) and samples
+    b = req(sched, 1, 100, 3)  # longer than the whole per-step budget
+    feeds = []
+    for _ in range(4):
+        batch = fake_step_chunked(sched)
+        assert batch.padded_tokens <= 40
+        rows = dict(zip(ids(batch.seqs), batch.new_lens))
+        assert rows[0] == 1  # A decodes in every step
+        feeds.append(rows.get(1))
+    assert feeds == [32, 32, 32, 4]  # B's prompt in chunks, capped by the chunk size and then what is left
+    assert len(b.output_token_ids) == 1 and len(a.output_token_ids) == 5
+
+
+def test_chunked_budget_is_shared_oldest_prefill_first_then_fcfs_admission():
+    sched = make(num_blocks=64, block_size=4, max_num_batched_tokens=48, max_num_seqs=8, chunked_prefill=True, prefill_chunk_tokens=32)
+    req(sched, 0, 50, 2)
+    req(sched, 1, 20, 2)
+    req(sched, 2, 8, 2)
+    batch = fake_step_chunked(sched)
+    assert list(zip(ids(batch.seqs), batch.new_lens)) == [(0, 32), (1, 16)]  # 48 tokens; request 2 waits
+    batch = fake_step_chunked(sched)
+    assert list(zip(ids(batch.seqs), batch.new_lens)) == [(0, 18), (1, 4), (2, 8)]
+    assert batch.is_prefill
+
+
+def test_chunked_mode_admits_prompts_longer_than_the_budget():
+    sched = make(num_blocks=64, block_size=16, max_num_batched_tokens=128, chunked_prefill=True)
+    req(sched, 0, 300, 5)  # alternating mode rejects this (tests/test_phase4_scheduler.py:221-224)
+    while sched.has_unfinished():
+        fake_step_chunked(sched)
+    assert sched.allocator.num_free_blocks == 64
+
+
+@settings(deadline=None, max_examples=200)
+@given(
+    workload=st.lists(st.tuples(st.integers(1, 60), st.integers(1, 30), st.integers(0, 25)), min_size=1, max_size=14),
+    num_blocks=st.integers(4, 24),
+    block_size=st.sampled_from([1, 2, 4, 8]),
+    max_num_seqs=st.integers(1, 8),
+    budget=st.integers(8, 120),
+    chunk=st.integers(1, 48),
+    watermark=st.integers(0, 3),
+)
+def test_chunked_random_workloads_never_deadlock_or_leak(workload, num_blocks, block_size, max_num_seqs, budget,
+                                                         chunk, watermark):  # fmt: skip
+    sched = make(num_blocks=num_blocks, block_size=block_size, max_num_seqs=max_num_seqs,
+                 max_num_batched_tokens=max(budget, max_num_seqs), watermark_blocks=watermark,
+                 chunked_prefill=True, prefill_chunk_tokens=chunk)  # fmt: skip
+    alloc = sched.allocator
+    pending = sorted(enumerate(workload), key=lambda x: x[1][2])
+    accepted = []
+    step = 0
+    while True:
+        while pending and pending[0][1][2] <= step:
+            i, (p, m, _) = pending.pop(0)
+            seq = Sequence(i, [1] * p, sampling=SamplingParams(max_tokens=m))
+            if sched.rejection_reason(seq):
+                with pytest.raises(RequestRejected):
+                    sched.add_request(seq)
+            else:
+                sched.add_request(seq)
+                accepted.append(seq)
+        if not pending and not sched.has_unfinished():
+            break
+        batch = fake_step_chunked(sched)
+        assert batch is not None or pending, "deadlock: work remains but nothing is schedulable"
+        step += 1
+        assert step < 50_000, "livelock"
+        if batch is not None:
+            assert batch.padded_tokens <= sched.config.max_num_batched_tokens
+            assert all(1 <= n <= max(1, chunk) or n == 1 for n in batch.new_lens)
+        assert len(sched.running) <= max_num_seqs
+        owned = [b for s in sched.running for b in s.block_table]
+        assert len(owned) == len(set(owned)) and alloc.num_free_blocks + len(owned) == alloc.num_blocks
+        for s in sched.running:
+            assert len(s.block_table) >= cdiv(s.num_cached_tokens, block_size)
+    assert all(s.status is SequenceStatus.FINISHED and len(s.output_token_ids) == s.sampling.max_tokens for s in accepted)
+    assert alloc.num_free_blocks == alloc.num_blocks

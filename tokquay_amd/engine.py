@@ -143,18 +143,24 @@ class Engine:
         st.peak_used_blocks = max(st.peak_used_blocks, self.allocator.num_used_blocks)
         st.num_preemptions = self.scheduler.num_preemptions
         st.positions_discarded = self.scheduler.num_discarded_positions
-        st.positions_computed += sum(s.num_uncached_tokens for s in batch.seqs)
+        fed = batch.new_lens or [s.num_uncached_tokens for s in batch.seqs]
+        st.positions_computed += sum(fed)
         st.positions_padded += batch.padded_tokens
 
         if self.graphs is not None and not batch.is_prefill:
             logits = self.graphs.forward(batch.seqs)
         else:
-            logits = paged_forward(self.model, self.allocator, batch.seqs)
+            logits = paged_forward(self.model, self.allocator, batch.seqs, batch.new_lens)
         self.last_step = StepInfo(batch.is_prefill, len(batch.seqs), batch.padded_tokens, self.kv_snapshot())
-        tokens = self._sample(batch.seqs, logits)
+        # A sequence samples once all its tokens are cached; a chunked prompt part-way through does not.
+        done = [i for i, s in enumerate(batch.seqs) if s.num_cached_tokens == s.num_tokens]
+        if len(done) < len(batch.seqs):
+            logits = logits[done]
+        seqs = [batch.seqs[i] for i in done]
+        tokens = self._sample(seqs, logits) if seqs else []
 
         events = []
-        for seq, tok in zip(batch.seqs, tokens):
+        for seq, tok in zip(seqs, tokens):
             seq.append_token(tok)
             reason = finish_reason_for(seq, tok, self.eos_token_id)
             if reason:
