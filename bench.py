@@ -300,12 +300,15 @@ def main() -> int:
     from tokquay_amd.weights import random_state_dict
 
     torch.manual_seed(0)
-    steps_needed = args.warmup + 2 * args.steps  # graph-replayed timed steps, then eager kernel-timing steps
+    # Warm-up, timed graph-replayed steps, eager kernel-timing steps, and the few steps the
+    # pipelined engine launches ahead or drains around them.
+    steps_needed = args.warmup + 2 * args.steps + 4
     engine, model = build_engine(steps_needed)
     engine.allocator.decode_partition_tokens = args.partition_tokens
 
     for _ in range(args.warmup):
         engine.step()
+    engine.drain()  # nothing in flight: every sequence's tokens are on the host
     if args.pmc_probe:
         x = torch.randn(1 << 28, device="cuda")  # 1 GiB
         y = torch.empty_like(x)
@@ -327,18 +330,24 @@ def main() -> int:
         cpu_state = snapshot_for_cpu(engine, running, args.cpu_seqs, spare_per_seq=args.cpu_steps // 16 + 2)
         log(f"copied {cpu_state[0].shape[0]} blocks for the CPU sample in {time.perf_counter() - t0:.1f} s")
 
+    # The step after the CPU snapshot (its ids are what the CPU sample's first step must give).
+    # The engine launches the following step ahead, so the timed region starts in steady state.
+    first_ids = [e.token_id for e in engine.step()]
+
     # Timed region: K decode steps through Engine.step, replayed from the captured HIP graph.
+    # The step in flight at the start is finished before the clock starts; the step launched
+    # ahead by the last call is finished inside it: K steps of GPU work, K steps of tokens.
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    first_ids = None
+    emitted = 0
     for k in range(args.steps):
-        events = engine.step()
-        if k == 0:
-            first_ids = [e.token_id for e in events]
+        emitted += len(engine.step())
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    assert emitted == N_SEQS * args.steps, emitted
     ms_per_step = elapsed * 1e3 / args.steps
-    tok_s = N_SEQS * args.steps / elapsed
+    tok_s = emitted / elapsed
+    engine.drain()
 
     # Kernel timing: K more decode steps run eagerly, every decode launch timed by HIP events
     # the launch itself records at the start and end of its kernels.

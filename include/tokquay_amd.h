@@ -8,6 +8,10 @@
  *   tq_paged_decode   one-query-per-sequence attention straight off the pool
  *   tq_paged_prefill  causal (chunked) prefill attention straight off the pool
  *
+ * plus the greedy-sampling reduction that ends a decode step:
+ *
+ *   tq_argmax_rows    index of each logit row's maximum
+ *
  * KV pool layout (identical to the reference's, bit for bit):
  *
  *   pool[num_blocks][num_layers][2][num_heads][block_size][head_dim]  fp32,
@@ -155,6 +159,21 @@ tq_status tq_paged_prefill(float* out, int64_t out_row_stride,
                            const int32_t* cu_seqlens_q, const int32_t* q_start,
                            int32_t num_seqs, int32_t num_q_rows, int32_t max_query_len,
                            float scale, int32_t* d_error, void* stream);
+
+/*
+ * Greedy sampling over a batch of logit rows:
+ *
+ *   out[r] = the lowest column c with logits[r * row_stride + c] maximal,  c < num_cols
+ *
+ * with the reference's order: NaN ranks above every number (the first NaN
+ * wins) and -0 ties +0. out is int64[num_rows]. num_cols in [1, 2^30];
+ * row_stride >= num_cols (elements).
+ *
+ * Replaces the batched `logits.argmax(-1)` of Engine._sample
+ * (tokquay/engine.py:190), so a decode step hands back only [B] token ids.
+ */
+tq_status tq_argmax_rows(int64_t* out, const float* logits, int64_t num_rows, int64_t num_cols,
+                         int64_t row_stride, void* stream);
 
 #ifdef __cplusplus
 }

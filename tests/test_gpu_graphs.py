@@ -88,8 +88,9 @@ def test_engine_with_and_without_graphs_emits_the_same_tokens(model):
     rng = random.Random(1)
     reqs = [([rng.randrange(50256) for _ in range(rng.randint(4, 50))], rng.randint(5, 30)) for _ in range(10)]
     outs = []
-    for use_graphs in (True, False):
-        engine = Engine(model, BlockAllocator(model.cfg, 128, 16, device="cuda"), use_graphs=use_graphs)
+    for use_graphs, pipeline in ((True, True), (True, False), (False, False)):
+        engine = Engine(model, BlockAllocator(model.cfg, 128, 16, device="cuda"), use_graphs=use_graphs,
+                        pipeline=pipeline)  # fmt: skip
         seqs = []
         for i, (p, n) in enumerate(reqs):
             seqs.append(engine.add_request(p, SamplingParams(max_tokens=n, ignore_eos=True)))
@@ -99,4 +100,5 @@ def test_engine_with_and_without_graphs_emits_the_same_tokens(model):
         outs.append([s.output_token_ids for s in seqs])
         if use_graphs:
             assert engine.graphs.graphs, "no decode step went through a graph"
-    assert outs[0] == outs[1]
+        assert (engine.stats.lookahead_steps > 0) == pipeline
+    assert outs[0] == outs[1] == outs[2]

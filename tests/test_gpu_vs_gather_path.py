@@ -47,6 +47,7 @@ def test_hip_engine_beats_the_reference_gather_path():
         engine.step()
     for _ in range(2):
         engine.step()  # graph capture + warm-up
+    engine.drain()  # the step launched ahead: afterwards every token is on the host
     seqs = list(engine.scheduler.running)
     assert len(seqs) == N
     state = [(list(s.block_table), s.num_cached_tokens, list(s.token_ids)) for s in seqs]

@@ -70,6 +70,10 @@ SIGNATURES: dict[str, tuple] = {
             ctypes.c_float, c_i32p, ctypes.c_void_p,  # scale, d_error, stream
         ],
     ),
+    "tq_argmax_rows": (
+        ctypes.c_int,
+        [c_i64p, c_f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p],  # out, logits, rows, cols, row_stride, stream
+    ),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -8,8 +8,12 @@ HIP graph and replays it.
 
 What changes between steps lives in static device buffers at fixed addresses,
 refreshed by one host-to-device copy per step: token ids, positions, slots,
-block tables (``n_positions / block_size`` columns, padded with block 0) and
-context lengths. The decode kernel's grid is sized for ``n_positions`` and its
+block tables (``n_positions / block_size`` columns, padded with block 0),
+context lengths and source rows. The graph ends with the greedy argmax of every
+row (``tq_argmax_rows``) into a static token buffer; a row whose source row is
+``r >= 0`` feeds the token the previous replay chose for its row ``r`` instead
+of a host-supplied id, so a step can be launched before the host has read the
+previous step's tokens. The decode kernel's grid is sized for ``n_positions`` and its
 waves skip partitions past each sequence's real context, so one graph serves
 every context length. Rows past the live batch are padding: slot -1 (the cache
 write skips them) and context 0 (the decode kernel writes zeros); their logits
@@ -26,7 +30,7 @@ import math
 import numpy as np
 import torch
 
-from tokquay_amd import _lib
+from tokquay_amd import _lib, ops
 from tokquay_amd.kv_cache import HEAD_DIM, BlockAllocator, cdiv
 from tokquay_amd.sequence import Sequence
 
@@ -48,12 +52,14 @@ class StaticDecodeBatch:
         self.max_blocks = cdiv(n_positions, self.block_size)
         dev = pool.device
         cap, mb = capacity, self.max_blocks
-        self.d64 = torch.zeros(3 * cap, dtype=torch.int64, device=dev)  # ids | positions | slots
+        self.d64 = torch.zeros(4 * cap, dtype=torch.int64, device=dev)  # ids | positions | slots | source rows
         self.d32 = torch.zeros(cap * mb + cap, dtype=torch.int32, device=dev)  # tables | context lengths
-        self.h64 = torch.zeros(3 * cap, dtype=torch.int64, pin_memory=True)
+        self.h64 = torch.zeros(4 * cap, dtype=torch.int64, pin_memory=True)
         self.h32 = torch.zeros(cap * mb + cap, dtype=torch.int32, pin_memory=True)
         self.copied = torch.cuda.Event()
-        self.ids, self.positions, self.slots = self.d64[:cap], self.d64[cap : 2 * cap], self.d64[2 * cap :]
+        self.ids, self.positions = self.d64[:cap], self.d64[cap : 2 * cap]
+        self.slots, self.src = self.d64[2 * cap : 3 * cap], self.d64[3 * cap :]
+        self.tokens = torch.zeros(cap, dtype=torch.int64, device=dev)  # greedy ids of the latest replay
         self.tables = self.d32[: cap * mb].view(cap, mb)
         self.context_lens = self.d32[cap * mb :]
         n_head = pool.shape[3]
@@ -71,11 +77,18 @@ class StaticDecodeBatch:
             b *= 2
         return out
 
-    def fill(self, seqs: list[Sequence], bucket: int) -> None:
-        """Write this step's metadata for ``seqs`` (each feeding its one uncached token) and pad to ``bucket``."""
+    def fill(self, seqs: list[Sequence], bucket: int, src_rows: list[int] | None = None) -> None:
+        """Write this step's metadata for ``seqs`` and pad to ``bucket``.
+
+        Without ``src_rows`` each sequence feeds its one uncached token. With them, each
+        sequence feeds the token the previous replay chose for row ``src_rows[i]``, which
+        the host has not appended yet (so the sequence has no uncached token)."""
         self.copied.synchronize()  # the previous step's copy has left the staging buffers
         cap, mb, bs = self.capacity, self.max_blocks, self.block_size
         n = len(seqs)
+        pending = 1 if src_rows is None else 0
+        if src_rows is not None and (len(src_rows) != n or (n and not 0 <= min(src_rows) <= max(src_rows) < cap)):
+            raise ValueError(f"src_rows needs one entry in [0, {cap}) per sequence")
         a64 = self.h64.numpy()
         a32 = self.h32.numpy()
         tables = a32[: cap * mb].reshape(cap, mb)
@@ -83,7 +96,7 @@ class StaticDecodeBatch:
         live = {}
         for i, s in enumerate(seqs):
             p = s.num_cached_tokens
-            if s.num_tokens - p != 1:
+            if s.num_tokens - p != pending:
                 raise ValueError("graph decode steps feed exactly one token per sequence")
             row, known = self._rows.get(s.seq_id, (None, -1))
             tbl = s.block_table
@@ -96,9 +109,15 @@ class StaticDecodeBatch:
             tables[i] = row
         self._rows = live
         pos = np.fromiter((s.num_cached_tokens for s in seqs), dtype=np.int64, count=n)
-        last = np.fromiter(((s.output_token_ids or s.prompt_token_ids)[-1] for s in seqs), dtype=np.int64, count=n)
         blk = tables[np.arange(n), pos // bs].astype(np.int64)
-        a64[:n] = last  # the token at position num_cached_tokens is the sequence's last one
+        if src_rows is None:
+            # The token at position num_cached_tokens is the sequence's last one.
+            a64[:n] = np.fromiter(((s.output_token_ids or s.prompt_token_ids)[-1] for s in seqs), np.int64, n)
+            a64[3 * cap : 3 * cap + n] = -1
+        else:
+            a64[:n] = 0
+            a64[3 * cap : 3 * cap + n] = src_rows
+        a64[3 * cap + n : 3 * cap + bucket] = -1
         a64[cap : cap + n] = pos
         a64[2 * cap : 2 * cap + n] = blk * bs + pos % bs
         a32[cap * mb : cap * mb + n] = pos + 1
@@ -151,20 +170,31 @@ class DecodeGraphs:
         self.static = StaticDecodeBatch(allocator, bucket_for(max_batch), model.cfg.n_positions)
         self.graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
 
+    @property
+    def capacity(self) -> int:
+        return self.static.capacity
+
     def _forward(self, rows: int) -> torch.Tensor:
         m, s = self.model, self.static
         view = s.view(rows)
-        x = m.wte(s.ids[:rows]) + m.wpe(s.positions[:rows])
+        src = s.src[:rows]
+        ids = torch.where(src >= 0, s.tokens.index_select(0, src.clamp(min=0)), s.ids[:rows])
+        x = m.wte(ids) + m.wpe(s.positions[:rows])
         for i, block in enumerate(m.h):
             x = block(x, view, i)
-        return m.ln_f(x) @ m.wte.weight.T
+        logits = m.ln_f(x) @ m.wte.weight.T
+        ops.argmax_rows(logits, out=s.tokens[:rows])
+        return logits
 
     def _capture(self, rows: int) -> None:
+        s = self.static
+        tokens = s.tokens.clone()  # the warm-up runs overwrite what this step's source rows read
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):  # warm-up launches (same inputs: the K/V writes are idempotent)
             for _ in range(2):
                 self._forward(rows)
+                s.tokens.copy_(tokens)
         torch.cuda.current_stream().wait_stream(side)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
@@ -172,18 +202,25 @@ class DecodeGraphs:
         self.graphs[rows] = (graph, logits)
 
     @torch.no_grad()
-    def forward(self, seqs: list[Sequence]) -> torch.Tensor:
-        """Logits ``[len(seqs), vocab]`` of one decode step; advances ``num_cached_tokens``."""
+    def launch(self, seqs: list[Sequence], src_rows: list[int] | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """Enqueue one decode step; returns views of its logits ``[n, vocab]`` and greedy ids ``[n]``
+        (valid until the next launch) and advances ``num_cached_tokens``. ``src_rows``: see
+        ``StaticDecodeBatch.fill``."""
         rows = bucket_for(len(seqs))
         if rows > self.static.capacity:
             raise ValueError(f"{len(seqs)} sequences exceed the graph capacity {self.static.capacity}")
-        self.static.fill(seqs, rows)
+        self.static.fill(seqs, rows, src_rows)
         if rows not in self.graphs:
             self._capture(rows)
         graph, logits = self.graphs[rows]
         graph.replay()
         for s in seqs:
             s.num_cached_tokens += 1
-        return logits[: len(seqs)]
+        n = len(seqs)
+        return logits[:n], self.static.tokens[:n]
+
+    def forward(self, seqs: list[Sequence]) -> torch.Tensor:
+        """Logits ``[len(seqs), vocab]`` of one decode step; advances ``num_cached_tokens``."""
+        return self.launch(seqs)[0]
 
 

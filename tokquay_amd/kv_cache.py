@@ -97,9 +97,10 @@ class BlockAllocator:
     def can_append_slot(self, seq: Sequence) -> bool:
         return self.blocks_needed(seq.num_tokens) - len(seq.block_table) <= self.num_free_blocks
 
-    def append_slot(self, seq: Sequence) -> bool:
-        """Grow the table to cover ``seq.num_tokens`` positions; True if a block was taken."""
-        missing = self.blocks_needed(seq.num_tokens) - len(seq.block_table)
+    def append_slot(self, seq: Sequence, num_tokens: int | None = None) -> bool:
+        """Grow the table to cover ``num_tokens`` positions (default ``seq.num_tokens``); True if a
+        block was taken."""
+        missing = self.blocks_needed(seq.num_tokens if num_tokens is None else num_tokens) - len(seq.block_table)
         if missing <= 0:
             return False
         seq.block_table.extend(self._take(missing))

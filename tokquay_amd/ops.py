@@ -172,3 +172,25 @@ def paged_prefill(
         err, _stream(pool.device),
     )  # fmt: skip
     _lib.check(st, "tq_paged_prefill")
+
+
+def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Greedy ids ``[R]`` (int64) of float32 logits ``[R, V]``: the reference's ``logits.argmax(-1)``
+    (tokquay/engine.py:190) - the lowest index of each row's maximum, NaN above every number."""
+    if logits.dtype != torch.float32 or not logits.is_cuda or logits.dim() != 2:
+        raise ValueError("logits must be a float32 [rows, vocab] tensor on a HIP device")
+    rows, cols = logits.shape
+    if cols < 1:
+        raise ValueError("logits need at least one column")
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int64, device=logits.device)
+    elif out.dtype != torch.int64 or out.device != logits.device or out.dim() != 1 or out.numel() != rows:
+        raise ValueError(f"out must be an int64 [{rows}] tensor on {logits.device}")
+    elif rows > 1 and out.stride(0) != 1:
+        raise ValueError("out must be contiguous")
+    stride = logits.stride(0) if rows > 1 else cols
+    if cols > 1 and logits.stride(1) != 1:
+        raise ValueError("logits rows must be contiguous")
+    st = _lib.lib().tq_argmax_rows(out.data_ptr(), logits.data_ptr(), rows, cols, stride, _stream(logits.device))
+    _lib.check(st, "tq_argmax_rows")
+    return out
