@@ -46,12 +46,14 @@ def log(msg: str) -> None:
 
 
 def decode_bytes(ctxs: list[int], n_head: int = 12, d: int = 64, bs: int = BLOCK) -> int:
-    """Algorithmic HBM bytes of one decode-attention layer call: every cached K and V row once,
-    q in and out, the block-table entries and context lengths."""
+    """Algorithmic HBM bytes of one decode-attention layer call (tq_paged_decode_write): every K and
+    V row of the context read once (the new token's from the projection output), the new token's
+    K and V written into the pool, q in and out, the block-table entries and context lengths."""
     kv = sum(2 * c * n_head * d * 4 for c in ctxs)
+    new_kv = 2 * len(ctxs) * n_head * d * 4
     qo = 2 * len(ctxs) * n_head * d * 4
     meta = sum(-(-c // bs) * 4 for c in ctxs) + 4 * len(ctxs)
-    return kv + qo + meta
+    return kv + new_kv + qo + meta
 
 
 class LaunchTimer:

@@ -6,6 +6,7 @@
  *
  *   tq_cache_write    scatter each new token's K/V rows into the block pool
  *   tq_paged_decode   one-query-per-sequence attention straight off the pool
+ *   tq_paged_decode_write  the same, with the new token's cache write folded in
  *   tq_paged_prefill  causal (chunked) prefill attention straight off the pool
  *
  * plus the greedy-sampling reduction that ends a decode step:
@@ -71,7 +72,7 @@ const char* tq_last_hip_error(void);
 
 /*
  * Arms two hipEvent_t handles (passed as void*; either may be NULL) for the
- * calling thread's next tq_paged_decode or tq_paged_prefill call: the start
+ * calling thread's next tq_paged_decode, tq_paged_decode_write or tq_paged_prefill call: the start
  * event is recorded when that call's first kernel starts and the stop event
  * when its last kernel ends, so hipEventElapsedTime gives the kernels' own
  * duration, without launch gaps. That call disarms them, whatever it returns.
@@ -128,6 +129,36 @@ tq_status tq_paged_decode(float* out, int64_t out_row_stride,
                           float scale, int32_t partition_tokens,
                           void* workspace, size_t workspace_bytes,
                           int32_t* d_error, void* stream);
+
+/*
+ * Paged decode with the cache write of the new token folded in. For every row b
+ * with context_lens[b] = n > 0 the new token sits at position p = n - 1, in slot
+ * block_tables[b * block_table_stride + p / block_size] * block_size + p % block_size:
+ *
+ *   pool[slot / block_size][layer][0][h][slot % block_size][:] = k_new[b * k_new_row_stride + h * 64 + :]
+ *   pool[slot / block_size][layer][1][h][slot % block_size][:] = v_new[b * v_new_row_stride + h * 64 + :]
+ *
+ * for every head h, then out as tq_paged_decode computes it over positions
+ * 0..n-1. Output and pool are bit-identical to tq_cache_write (slot_mapping[b]
+ * = that slot) followed by tq_paged_decode. Rows with n == 0 write nothing. The
+ * same workspace as tq_paged_decode (tq_paged_decode_workspace_size).
+ *
+ * Replaces PagedBatch.write (tokquay/kv_cache.py:228-232) for rows that feed one
+ * token, together with what tq_paged_decode replaces (tokquay/kv_cache.py:208-214,
+ * :234-242; tokquay/model.py:94-96).
+ */
+tq_status tq_paged_decode_write(float* out, int64_t out_row_stride,
+                                const float* q, int64_t q_row_stride,
+                                const float* k_new, int64_t k_new_row_stride,
+                                const float* v_new, int64_t v_new_row_stride,
+                                float* pool, int64_t num_blocks, int32_t num_layers,
+                                int32_t num_heads, int32_t block_size, int32_t head_dim, int32_t layer,
+                                const int32_t* block_tables, int64_t block_table_stride,
+                                int32_t max_blocks_per_seq,
+                                const int32_t* context_lens, int32_t num_seqs, int32_t max_context_len,
+                                float scale, int32_t partition_tokens,
+                                void* workspace, size_t workspace_bytes,
+                                int32_t* d_error, void* stream);
 
 /* Bytes of workspace tq_paged_decode needs for these sizes (0 if none). */
 size_t tq_paged_decode_workspace_size(int32_t num_seqs, int32_t num_heads, int32_t head_dim,

@@ -33,7 +33,8 @@ def lib():
 
 def test_header_declares_the_three_kernels_and_helpers():
     names = declared_functions()
-    for n in ("tq_cache_write", "tq_paged_decode", "tq_paged_prefill", "tq_paged_decode_workspace_size",
+    for n in ("tq_cache_write", "tq_paged_decode", "tq_paged_decode_write", "tq_paged_prefill", "tq_argmax_rows",
+              "tq_paged_decode_workspace_size",
               "tq_status_string", "tq_abi_version", "tq_last_hip_error"):  # fmt: skip
         assert n in names
 
@@ -67,6 +68,15 @@ def test_invalid_arguments_are_rejected_before_any_launch(lib):
     # decode: partition not a multiple of 16
     assert lib.tq_paged_decode(None, 768, None, 768, None, 8, 1, 12, 16, 64, 0, None, 4, 4, None, 2, 64,
                                0.125, 24, None, 0, None, None) == 1  # fmt: skip
+    # decode with the write folded in: null new rows with sequences to do
+    assert lib.tq_paged_decode_write(None, 768, None, 2304, None, 2304, None, 2304, None, 8, 1, 12, 16, 64, 0,
+                                     None, 4, 4, None, 2, 64, 0.125, 0, None, 0, None, None) == 1  # fmt: skip
+    # ... new-row stride shorter than a row of heads
+    assert lib.tq_paged_decode_write(None, 768, None, 2304, 16, 700, 16, 2304, None, 8, 1, 12, 16, 64, 0,
+                                     None, 4, 4, None, 2, 64, 0.125, 0, None, 0, None, None) == 1  # fmt: skip
+    # ... zero sequences is a no-op
+    assert lib.tq_paged_decode_write(None, 768, None, 2304, None, 2304, None, 2304, None, 8, 1, 12, 16, 64, 0,
+                                     None, 4, 4, None, 0, 64, 0.125, 0, None, 0, None, None) == 0  # fmt: skip
     # prefill: zero sequences is a no-op
     assert lib.tq_paged_prefill(None, 768, None, 768, None, 8, 1, 12, 16, 64, 0, None, 4, 4, None, None,
                                 0, 0, 0, 0.125, None, None) == 0  # fmt: skip

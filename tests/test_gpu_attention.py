@@ -64,6 +64,45 @@ def test_decode_edge_contexts(block_size, partition_tokens):
     check(sc, partition_tokens)
 
 
+@pytest.mark.parametrize("block_size", [1, 16, 32])
+@pytest.mark.parametrize("partition_tokens", [0, 16, 1024])
+def test_decode_write_equals_cache_write_then_decode(block_size, partition_tokens):
+    """tq_paged_decode_write == tq_cache_write + tq_paged_decode, bit for bit (output and pool), with
+    a padding row (context 0, writes nothing) and the new position at every block offset class."""
+    from tokquay_amd import ops
+
+    ctx = [1, 2, block_size, block_size + 1, 77, 300, 0, 1024]
+    n_layer, layer = 2, 1
+    nb = sum(cdiv(c, block_size) for c in ctx) + 2
+    pool0 = torch.randn(nb, n_layer, 2, 12, block_size, 64, generator=torch.Generator().manual_seed(5)) * 50
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(6)).tolist()
+    width = cdiv(1024, block_size)
+    tables = torch.zeros(len(ctx), width, dtype=torch.int32)
+    slots, i = [], 0
+    for b, c in enumerate(ctx):
+        n = cdiv(c, block_size)
+        tables[b, :n] = torch.tensor(perm[i : i + n], dtype=torch.int32)
+        i += n
+        slots.append(int(tables[b, (c - 1) // block_size]) * block_size + (c - 1) % block_size if c else -1)
+    g = torch.Generator().manual_seed(7)
+    qkv = torch.randn(len(ctx), 3 * 768, generator=g).cuda()
+    q, k, v = qkv[:, :768], qkv[:, 768:1536], qkv[:, 1536:]
+    tables, cl = tables.cuda(), torch.tensor(ctx, dtype=torch.int32, device="cuda")
+    sm = torch.tensor(slots, dtype=torch.int64, device="cuda")
+    pa, pb = pool0.cuda(), pool0.cuda()
+    oa, ob = torch.empty(len(ctx), 768, device="cuda"), torch.empty(len(ctx), 768, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ops.cache_write(pa, layer, k, v, sm, err)
+    ops.paged_decode(oa, q, pa, layer, tables, cl, 1024, partition_tokens=partition_tokens, d_error=err)
+    ops.paged_decode(ob, q, pb, layer, tables, cl, 1024, partition_tokens=partition_tokens, d_error=err,
+                     k_new=k, v_new=v)  # fmt: skip
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    assert torch.equal(oa, ob)
+    assert torch.equal(pa, pb)
+    assert not torch.equal(pb, pool0.cuda())  # the new rows did land
+
+
 def test_decode_config4_scale():
     """256 sequences, contexts ~ U[256, 1024], block size 16 (the decode-throughput workload's shape)."""
     rng = random.Random(4)
@@ -137,6 +176,27 @@ def test_out_of_range_block_id_is_reported_not_followed():
     torch.cuda.synchronize()
     assert int(err.item()) & 1
     assert torch.isfinite(out).all()
+
+
+def test_write_variant_skips_an_out_of_range_block_id():
+    """The new position's block id is past the pool: the row is reported and nothing is written."""
+    from tokquay_amd import ops
+
+    pool = torch.zeros(8, 1, 2, 12, 16, 64, device="cuda")
+    qkv = torch.randn(2, 3 * 768, device="cuda")
+    out = torch.empty(2, 768, device="cuda")
+    tables = torch.tensor([[0, 1], [2, 8 + 5]], dtype=torch.int32, device="cuda")
+    ctx = torch.tensor([20, 20], dtype=torch.int32, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ops.paged_decode(out, qkv[:, :768], pool, 0, tables, ctx, 20, d_error=err, k_new=qkv[:, 768:1536],
+                     v_new=qkv[:, 1536:])  # fmt: skip
+    torch.cuda.synchronize()
+    assert int(err.item()) & 1
+    want = torch.zeros_like(pool)
+    want[1, 0, 0, :, 3] = qkv[0, 768:1536].view(12, 64)  # row 0: position 19 = block 1, offset 3
+    want[1, 0, 1, :, 3] = qkv[0, 1536:].view(12, 64)
+    assert torch.equal(pool, want)
+    assert torch.isfinite(out[0]).all()
 
 
 def test_host_side_argument_errors_raise():

@@ -24,6 +24,12 @@
 // :234-242) and the masked softmax attention of Attention.forward
 // (tokquay/model.py:94-96), for a query at position ctx-1 that sees keys
 // 0..ctx-1 (tokquay/kv_cache.py:188, :213-214).
+//
+// The write variant also does the cache write of the one new token per sequence
+// (PagedBatch.write, tokquay/kv_cache.py:228-232): the workgroups whose
+// partition holds position ctx-1 read that position's K/V from the projection
+// output instead of the pool, and store it (one head each) into the pool after
+// their last read, so no separate cache-write pass over the new rows is needed.
 
 #include <hip/hip_ext.h>
 #include <math.h>
@@ -56,6 +62,11 @@ struct DecodeArgs {
   const int32_t* context_lens;
   float* partials;  // [num_seqs][num_heads][max_parts][kPartialStride]
   int32_t* d_error;
+  float* pool_layer_w;  // the write variant: writable alias of pool_layer
+  const float* k_new;   // the write variant: row b's new K at k_new + b * k_new_stride (heads contiguous)
+  const float* v_new;
+  int64_t k_new_stride;
+  int64_t v_new_stride;
   float scale;
   int32_t num_blocks;
   int32_t num_heads;
@@ -115,10 +126,13 @@ __device__ __forceinline__ PartitionBlocks load_partition_blocks(const DecodeArg
 // Branch free: every lane loads from an in-bounds address (positions past
 // t_end re-read a position of the same block, bad block ids read block 0) and
 // invalid positions are zeroed by a select and reported through ok[j].
-template <int BS_CT>
+// In the write variant, position t_new is loaded from the new row (knew / vnew: this lane's dims of
+// it in the projection output) instead of from the pool, which the same kernel writes.
+template <int BS_CT, bool WRITE>
 __device__ __forceinline__ void load_chunk(const DecodeArgs& a, const int32_t* bt, const PartitionBlocks& pb,
                                            const float* head_base, int bs, int t0, int t_end,
-                                           int r, float4 (&kx)[4], float4 (&vx)[4], bool (&ok)[4]) {
+                                           int r, float4 (&kx)[4], float4 (&vx)[4], bool (&ok)[4],
+                                           int t_new, const float* knew, const float* vnew) {
   const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
   if constexpr (BS_CT >= kChunk) {
     // The whole chunk sits in one block (t0 is a multiple of 16 and so is BS_CT).
@@ -129,9 +143,15 @@ __device__ __forceinline__ void load_chunk(const DecodeArgs& a, const int32_t* b
     float4 k_raw[4], v_raw[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float* p = base + (4 * j + r) * kHeadDim;
-      k_raw[j] = load_kv(p);
-      v_raw[j] = load_kv(p + a.kv_stride);
+      const float* pk = base + (4 * j + r) * kHeadDim;
+      const float* pv = pk + a.kv_stride;
+      if constexpr (WRITE) {
+        const bool is_new = t0 + 4 * j + r == t_new;
+        pk = is_new ? knew : pk;
+        pv = is_new ? vnew : pv;
+      }
+      k_raw[j] = load_kv(pk);
+      v_raw[j] = load_kv(pv);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -153,15 +173,46 @@ __device__ __forceinline__ void load_chunk(const DecodeArgs& a, const int32_t* b
         blk = 0;
       }
       ok[j] = blk_ok && t_req < t_end;
-      const float* p = head_base + blk * a.block_stride + (int64_t)(t - bi * bs) * kHeadDim;
-      k_raw[j] = load_kv(p);
-      v_raw[j] = load_kv(p + a.kv_stride);
+      const float* pk = head_base + blk * a.block_stride + (int64_t)(t - bi * bs) * kHeadDim;
+      const float* pv = pk + a.kv_stride;
+      if constexpr (WRITE) {
+        const bool is_new = t_req == t_new;
+        pk = is_new ? knew : pk;
+        pv = is_new ? vnew : pv;
+      }
+      k_raw[j] = load_kv(pk);
+      v_raw[j] = load_kv(pv);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       kx[j] = ok[j] ? k_raw[j] : zero;
       vx[j] = ok[j] ? v_raw[j] : zero;
     }
+  }
+}
+
+// Write variant: stores head h of the new row (position t_new) into its slot of the pool.
+// Lanes of DPP row 0 hold the 64 dims (a float4 each); a bad block id is reported and skipped.
+template <int BS_CT>
+__device__ __forceinline__ void write_new_row(const DecodeArgs& a, const int32_t* bt, const PartitionBlocks& pb,
+                                              int bs, int h, int t_new, int lane, int c, const float* knew,
+                                              const float* vnew) {
+  int64_t blk;
+  bool blk_ok;
+  if constexpr (BS_CT >= kChunk) {
+    const int slot = t_new / BS_CT - pb.first;  // wave-uniform; reported by load_partition_blocks
+    blk = __builtin_amdgcn_readlane(pb.id, slot);
+    blk_ok = __builtin_amdgcn_readlane(pb.ok, slot) != 0;
+  } else {
+    blk = bt[t_new / bs];
+    blk_ok = (uint64_t)blk < (uint64_t)a.num_blocks;
+    if (!blk_ok && lane == 0) flag_error(a.d_error, TQ_DEVERR_BLOCK_ID);
+  }
+  if (blk_ok && lane < kHeadDim / 4) {
+    float* dst = a.pool_layer_w + blk * a.block_stride + (int64_t)h * a.head_stride +
+                 (int64_t)(t_new % bs) * kHeadDim + c;
+    *reinterpret_cast<float4*>(dst) = *reinterpret_cast<const float4*>(knew);
+    *reinterpret_cast<float4*>(dst + a.kv_stride) = *reinterpret_cast<const float4*>(vnew);
   }
 }
 
@@ -203,7 +254,7 @@ __device__ __forceinline__ void consume_chunk(const float4 q4, const float4 (&kx
   }
 }
 
-template <int BS_CT>
+template <int BS_CT, bool WRITE>
 __global__ __launch_bounds__(kWave* kHeadsPerGroup) void decode_partition_kernel(const DecodeArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
   const int h = blockIdx.x * kHeadsPerGroup + (threadIdx.x / kWave);
@@ -236,6 +287,18 @@ __global__ __launch_bounds__(kWave* kHeadsPerGroup) void decode_partition_kernel
   PartitionBlocks pb{0, 0, 0};
   if constexpr (BS_CT >= kChunk) pb = load_partition_blocks<BS_CT>(a, bt, t_begin, t_end, lane);
 
+  int t_new = -1;  // the new position when this partition holds it (write variant)
+  const float* knew = nullptr;
+  const float* vnew = nullptr;
+  if constexpr (WRITE) {
+    // A clamped (invalid, already reported) length writes nothing.
+    if (ctx - 1 >= t_begin && ctx - 1 < t_end && a.context_lens[b] == ctx) {  // uniform across the wave
+      t_new = ctx - 1;
+      knew = a.k_new + (int64_t)b * a.k_new_stride + h * kHeadDim + c;
+      vnew = a.v_new + (int64_t)b * a.v_new_stride + h * kHeadDim + c;
+    }
+  }
+
   // kChunksPerIter chunks per iteration: all their loads are in flight before
   // the first chunk's math.
   for (int t0 = t_begin; t0 < t_end; t0 += kChunksPerIter * kChunk) {
@@ -244,7 +307,8 @@ __global__ __launch_bounds__(kWave* kHeadsPerGroup) void decode_partition_kernel
 #pragma unroll
     for (int c = 0; c < kChunksPerIter; ++c)
       if (c == 0 || t0 + c * kChunk < t_end)  // uniform across the wave
-        load_chunk<BS_CT>(a, bt, pb, head_base, bs, t0 + c * kChunk, t_end, r, kx[c], vx[c], ok[c]);
+        load_chunk<BS_CT, WRITE>(a, bt, pb, head_base, bs, t0 + c * kChunk, t_end, r, kx[c], vx[c], ok[c],
+                                 t_new, knew, vnew);
 #pragma unroll
     for (int c = 0; c < kChunksPerIter; ++c)
       if (c == 0 || t0 + c * kChunk < t_end) consume_chunk(q4, kx[c], vx[c], ok[c], m, l, acc);
@@ -269,6 +333,12 @@ __global__ __launch_bounds__(kWave* kHeadsPerGroup) void decode_partition_kernel
     acc.z = acc.z * ws + ao.z * wo;
     acc.w = acc.w * ws + ao.w * wo;
     m = mn;
+  }
+
+  // The new row goes into the pool last: a store waited on before the loop stalls each
+  // workgroup behind the saturated reads (measured: 3.4x slower launches).
+  if constexpr (WRITE) {
+    if (t_new >= 0) write_new_row<BS_CT>(a, bt, pb, bs, h, t_new, lane, c, knew, vnew);
   }
 
   const int nparts = (ctx + a.part_tokens - 1) / a.part_tokens;
@@ -322,7 +392,7 @@ int num_partitions(int32_t max_context_len, int part) {
   return max_context_len <= 0 ? 1 : (max_context_len + part - 1) / part;
 }
 
-template <int BS_CT>
+template <int BS_CT, bool WRITE>
 void launch_decode(const DecodeArgs& a, int num_seqs, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   const dim3 block(kWave * kHeadsPerGroup);
   const unsigned hgroups = (unsigned)((a.num_heads + kHeadsPerGroup - 1) / kHeadsPerGroup);
@@ -331,13 +401,14 @@ void launch_decode(const DecodeArgs& a, int num_seqs, hipStream_t stream, hipEve
   const dim3 merge_grid(hgroups, (unsigned)num_seqs);
   if (start == nullptr && stop == nullptr) {
     // The plain launch (what a HIP graph captures).
-    hipLaunchKernelGGL(decode_partition_kernel<BS_CT>, part_grid, block, 0, stream, a);
+    hipLaunchKernelGGL((decode_partition_kernel<BS_CT, WRITE>), part_grid, block, 0, stream, a);
     if (merge) hipLaunchKernelGGL(decode_merge_kernel, merge_grid, block, 0, stream, a);
     return;
   }
   // hipExtLaunchKernelGGL records the events at the dispatch's own start and end,
   // so a caller's timing covers exactly these kernels.
-  hipExtLaunchKernelGGL(decode_partition_kernel<BS_CT>, part_grid, block, 0, stream, start, merge ? nullptr : stop, 0, a);
+  hipExtLaunchKernelGGL((decode_partition_kernel<BS_CT, WRITE>), part_grid, block, 0, stream, start,
+                        merge ? nullptr : stop, 0, a);
   if (merge) hipExtLaunchKernelGGL(decode_merge_kernel, merge_grid, block, 0, stream, nullptr, stop, 0, a);
 }
 
@@ -355,19 +426,22 @@ extern "C" size_t tq_paged_decode_workspace_size(int32_t num_seqs, int32_t num_h
   return (size_t)num_seqs * num_heads * parts * kPartialStride * sizeof(float);
 }
 
-extern "C" tq_status tq_paged_decode(float* out, int64_t out_row_stride, const float* q,
-                                     int64_t q_row_stride, const float* pool, int64_t num_blocks,
-                                     int32_t num_layers, int32_t num_heads, int32_t block_size,
-                                     int32_t head_dim, int32_t layer, const int32_t* block_tables,
-                                     int64_t block_table_stride, int32_t max_blocks_per_seq,
-                                     const int32_t* context_lens, int32_t num_seqs,
-                                     int32_t max_context_len, float scale, int32_t partition_tokens,
-                                     void* workspace, size_t workspace_bytes, int32_t* d_error,
-                                     void* stream) {
-  using namespace tq;
+namespace tq {
+namespace {
+
+// Both decode entry points: k_new == nullptr is plain decode, otherwise the write variant.
+tq_status paged_decode_impl(float* out, int64_t out_row_stride, const float* q, int64_t q_row_stride,
+                            const float* k_new, int64_t k_new_row_stride, const float* v_new,
+                            int64_t v_new_row_stride, float* pool_w, const float* pool, int64_t num_blocks,
+                            int32_t num_layers, int32_t num_heads, int32_t block_size, int32_t head_dim,
+                            int32_t layer, const int32_t* block_tables, int64_t block_table_stride,
+                            int32_t max_blocks_per_seq, const int32_t* context_lens, int32_t num_seqs,
+                            int32_t max_context_len, float scale, int32_t partition_tokens, void* workspace,
+                            size_t workspace_bytes, int32_t* d_error, void* stream) {
   // Timing events apply to this call only, whatever it returns.
   const TimingEvents timing = take_timing_events();
   hipEvent_t t_start = timing.start, t_stop = timing.stop;
+  const bool write = k_new != nullptr;
   if (num_seqs < 0 || num_blocks < 1 || num_layers < 1 || num_heads < 1 || block_size < 1 ||
       head_dim < 1 || layer < 0 || layer >= num_layers || max_blocks_per_seq < 0 ||
       max_context_len < 0 || partition_tokens < 0 || partition_tokens % kChunk != 0 ||
@@ -421,12 +495,74 @@ extern "C" tq_status tq_paged_decode(float* out, int64_t out_row_stride, const f
   a.part_tokens = part;
   a.max_parts = parts;
 
+  a.pool_layer_w = write ? pool_w + g.layer_offset : nullptr;
+  a.k_new = k_new;
+  a.v_new = v_new;
+  a.k_new_stride = k_new_row_stride;
+  a.v_new_stride = v_new_row_stride;
+
   hipStream_t s = (hipStream_t)stream;
-  switch (block_size) {
-    case 16: launch_decode<16>(a, num_seqs, s, t_start, t_stop); break;
-    case 32: launch_decode<32>(a, num_seqs, s, t_start, t_stop); break;
-    default: launch_decode<0>(a, num_seqs, s, t_start, t_stop); break;
+  if (write) {
+    switch (block_size) {
+      case 16: launch_decode<16, true>(a, num_seqs, s, t_start, t_stop); break;
+      case 32: launch_decode<32, true>(a, num_seqs, s, t_start, t_stop); break;
+      default: launch_decode<0, true>(a, num_seqs, s, t_start, t_stop); break;
+    }
+  } else {
+    switch (block_size) {
+      case 16: launch_decode<16, false>(a, num_seqs, s, t_start, t_stop); break;
+      case 32: launch_decode<32, false>(a, num_seqs, s, t_start, t_stop); break;
+      default: launch_decode<0, false>(a, num_seqs, s, t_start, t_stop); break;
+    }
   }
   return check_launch();
+}
+
+}  // namespace
+}  // namespace tq
+
+extern "C" tq_status tq_paged_decode(float* out, int64_t out_row_stride, const float* q,
+                                     int64_t q_row_stride, const float* pool, int64_t num_blocks,
+                                     int32_t num_layers, int32_t num_heads, int32_t block_size,
+                                     int32_t head_dim, int32_t layer, const int32_t* block_tables,
+                                     int64_t block_table_stride, int32_t max_blocks_per_seq,
+                                     const int32_t* context_lens, int32_t num_seqs,
+                                     int32_t max_context_len, float scale, int32_t partition_tokens,
+                                     void* workspace, size_t workspace_bytes, int32_t* d_error,
+                                     void* stream) {
+  return tq::paged_decode_impl(out, out_row_stride, q, q_row_stride, nullptr, 0, nullptr, 0, nullptr, pool,
+                               num_blocks, num_layers, num_heads, block_size, head_dim, layer, block_tables,
+                               block_table_stride, max_blocks_per_seq, context_lens, num_seqs, max_context_len,
+                               scale, partition_tokens, workspace, workspace_bytes, d_error, stream);
+}
+
+extern "C" tq_status tq_paged_decode_write(float* out, int64_t out_row_stride, const float* q,
+                                           int64_t q_row_stride, const float* k_new, int64_t k_new_row_stride,
+                                           const float* v_new, int64_t v_new_row_stride, float* pool,
+                                           int64_t num_blocks, int32_t num_layers, int32_t num_heads,
+                                           int32_t block_size, int32_t head_dim, int32_t layer,
+                                           const int32_t* block_tables, int64_t block_table_stride,
+                                           int32_t max_blocks_per_seq, const int32_t* context_lens,
+                                           int32_t num_seqs, int32_t max_context_len, float scale,
+                                           int32_t partition_tokens, void* workspace, size_t workspace_bytes,
+                                           int32_t* d_error, void* stream) {
+  using namespace tq;
+  if (num_seqs > 0) {
+    const int64_t row = (int64_t)num_heads * head_dim;
+    if (k_new == nullptr || v_new == nullptr || pool == nullptr) {
+      take_timing_events();  // armed events apply to this call only
+      return TQ_ERR_INVALID_ARGUMENT;
+    }
+    if (k_new_row_stride < row || v_new_row_stride < row || k_new_row_stride % 4 != 0 ||
+        v_new_row_stride % 4 != 0 || ((uintptr_t)k_new | (uintptr_t)v_new) % 16 != 0) {
+      take_timing_events();
+      return TQ_ERR_INVALID_ARGUMENT;
+    }
+  }
+  return paged_decode_impl(out, out_row_stride, q, q_row_stride, num_seqs > 0 ? k_new : nullptr,
+                           k_new_row_stride, v_new, v_new_row_stride, pool, pool, num_blocks, num_layers,
+                           num_heads, block_size, head_dim, layer, block_tables, block_table_stride,
+                           max_blocks_per_seq, context_lens, num_seqs, max_context_len, scale, partition_tokens,
+                           workspace, workspace_bytes, d_error, stream);
 }
 

@@ -2,12 +2,12 @@
 
 A decode step (every sequence feeds one token) runs ~180 small launches from
 Python; at 256 sequences that host work is a third of the step. This module
-captures the whole decode forward (embeddings, 12 layers with the cache-write
-and paged-decode kernels, LM head) once per batch bucket (powers of two) into a
+captures the whole decode forward (embeddings, 12 layers with the paged-decode
+kernel that also writes the new K/V, LM head) once per batch bucket (powers of two) into a
 HIP graph and replays it.
 
 What changes between steps lives in static device buffers at fixed addresses,
-refreshed by one host-to-device copy per step: token ids, positions, slots,
+refreshed by one host-to-device copy per step: token ids, positions,
 block tables (``n_positions / block_size`` columns, padded with block 0),
 context lengths and source rows. The graph ends with the greedy argmax of every
 row (``tq_argmax_rows``) into a static token buffer; a row whose source row is
@@ -15,8 +15,8 @@ row (``tq_argmax_rows``) into a static token buffer; a row whose source row is
 of a host-supplied id, so a step can be launched before the host has read the
 previous step's tokens. The decode kernel's grid is sized for ``n_positions`` and its
 waves skip partitions past each sequence's real context, so one graph serves
-every context length. Rows past the live batch are padding: slot -1 (the cache
-write skips them) and context 0 (the decode kernel writes zeros); their logits
+every context length. Rows past the live batch are padding: context 0 (the
+decode kernel writes nothing to the pool and zeros to the output); their logits
 are ignored.
 
 No memset, host synchronisation or allocation happens inside the captured
@@ -52,13 +52,12 @@ class StaticDecodeBatch:
         self.max_blocks = cdiv(n_positions, self.block_size)
         dev = pool.device
         cap, mb = capacity, self.max_blocks
-        self.d64 = torch.zeros(4 * cap, dtype=torch.int64, device=dev)  # ids | positions | slots | source rows
+        self.d64 = torch.zeros(3 * cap, dtype=torch.int64, device=dev)  # ids | positions | source rows
         self.d32 = torch.zeros(cap * mb + cap, dtype=torch.int32, device=dev)  # tables | context lengths
-        self.h64 = torch.zeros(4 * cap, dtype=torch.int64, pin_memory=True)
+        self.h64 = torch.zeros(3 * cap, dtype=torch.int64, pin_memory=True)
         self.h32 = torch.zeros(cap * mb + cap, dtype=torch.int32, pin_memory=True)
         self.copied = torch.cuda.Event()
-        self.ids, self.positions = self.d64[:cap], self.d64[cap : 2 * cap]
-        self.slots, self.src = self.d64[2 * cap : 3 * cap], self.d64[3 * cap :]
+        self.ids, self.positions, self.src = self.d64[:cap], self.d64[cap : 2 * cap], self.d64[2 * cap :]
         self.tokens = torch.zeros(cap, dtype=torch.int64, device=dev)  # greedy ids of the latest replay
         self.tables = self.d32[: cap * mb].view(cap, mb)
         self.context_lens = self.d32[cap * mb :]
@@ -109,23 +108,24 @@ class StaticDecodeBatch:
             tables[i] = row
         self._rows = live
         pos = np.fromiter((s.num_cached_tokens for s in seqs), dtype=np.int64, count=n)
-        blk = tables[np.arange(n), pos // bs].astype(np.int64)
+        covered = np.fromiter((v[1] for v in live.values()), dtype=np.int64, count=n) * bs
+        if n and (pos >= np.minimum(covered, self.max_ctx)).any():
+            raise ValueError("a sequence's block table does not cover the position it feeds")
         if src_rows is None:
             # The token at position num_cached_tokens is the sequence's last one.
             a64[:n] = np.fromiter(((s.output_token_ids or s.prompt_token_ids)[-1] for s in seqs), np.int64, n)
-            a64[3 * cap : 3 * cap + n] = -1
+            a64[2 * cap : 2 * cap + n] = -1
         else:
             a64[:n] = 0
-            a64[3 * cap : 3 * cap + n] = src_rows
-        a64[3 * cap + n : 3 * cap + bucket] = -1
+            a64[2 * cap : 2 * cap + n] = src_rows
+        a64[2 * cap + n : 2 * cap + bucket] = -1
         a64[cap : cap + n] = pos
-        a64[2 * cap : 2 * cap + n] = blk * bs + pos % bs
+        # The decode kernel writes each row's new K/V into the slot of position pos (context pos + 1).
         a32[cap * mb : cap * mb + n] = pos + 1
         a64[n:bucket] = 0
         a64[cap + n : cap + bucket] = 0
-        a64[2 * cap + n : 2 * cap + bucket] = -1  # padded rows write nothing
         tables[n:bucket] = 0
-        a32[cap * mb + n : cap * mb + bucket] = 0  # and attend to nothing
+        a32[cap * mb + n : cap * mb + bucket] = 0  # padded rows write and attend to nothing
         self.d64.copy_(self.h64, non_blocking=True)
         self.d32.copy_(self.h32, non_blocking=True)
         self.copied.record()
@@ -150,14 +150,12 @@ class StaticDecodeView:
         stream = torch.cuda.current_stream(pool.device).cuda_stream
         err = s.error_word.data_ptr() if s.error_word is not None else None
         qp, pp = qkv.data_ptr(), pool.data_ptr()
-        _lib.check(L.tq_cache_write(pp, nb, n_layer, n_head, bs, d, layer, qp + 4 * C, 3 * C, qp + 8 * C, 3 * C,
-                                    s.slots.data_ptr(), n, err, stream), "tq_cache_write")  # fmt: skip
         _lib.check(
-            L.tq_paged_decode(out.data_ptr(), C, qp, 3 * C, pp, nb, n_layer, n_head, bs, d, layer,
-                              s.tables.data_ptr(), s.max_blocks, s.max_blocks, s.context_lens.data_ptr(), n,
-                              s.max_ctx, 1.0 / math.sqrt(d), 0, s.workspace.data_ptr(), s.workspace.numel(),
-                              err, stream),
-            "tq_paged_decode",
+            L.tq_paged_decode_write(out.data_ptr(), C, qp, 3 * C, qp + 4 * C, 3 * C, qp + 8 * C, 3 * C, pp, nb,
+                                    n_layer, n_head, bs, d, layer, s.tables.data_ptr(), s.max_blocks, s.max_blocks,
+                                    s.context_lens.data_ptr(), n, s.max_ctx, 1.0 / math.sqrt(d), 0,
+                                    s.workspace.data_ptr(), s.workspace.numel(), err, stream),
+            "tq_paged_decode_write",
         )  # fmt: skip
         return out
 

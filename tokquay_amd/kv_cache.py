@@ -340,8 +340,10 @@ class PagedBatch(BatchedKV):
 
         ``qkv`` is the fused projection output ``[N, 3*C]`` over packed rows, laid
         out ``[q | k | v]`` with heads contiguous inside each (tokquay/model.py:69-71).
-        Launches: cache write, then decode attention for the one-token rows and
-        prefill attention for the rest, all on the current stream.
+        Launches, all on the current stream: decode attention for the one-token rows
+        with their cache write folded in (``tq_paged_decode_write``), then - for the
+        rows of sequences feeding several tokens - their cache write and prefill
+        attention.
         """
         pool = self.pool
         nb, n_layer, _, n_head, bs, d = pool.shape
@@ -361,11 +363,6 @@ class PagedBatch(BatchedKV):
         qp, pp, op = qkv.data_ptr(), pool.data_ptr(), out.data_ptr()
         scale = 1.0 / math.sqrt(d)
 
-        _lib.check(
-            L.tq_cache_write(pp, nb, n_layer, n_head, bs, d, layer, qp + 4 * C, row3, qp + 8 * C, row3,
-                             self.slot_mapping.data_ptr(), N, err, stream),
-            "tq_cache_write",
-        )  # fmt: skip
         Bd = self.num_decode
         if Bd:
             if self._workspace is None:
@@ -374,13 +371,20 @@ class PagedBatch(BatchedKV):
             if PagedBatch.launch_hook is not None:
                 PagedBatch.launch_hook(self, "decode")
             _lib.check(
-                L.tq_paged_decode(op, C, qp, row3, pp, nb, n_layer, n_head, bs, d, layer,
-                                  self.decode_block_tables.data_ptr(), self._nbd, self._nbd,
-                                  self.decode_context_lens.data_ptr(), Bd, self.decode_max_ctx, scale,
-                                  self.partition_tokens, self._workspace.data_ptr(), self._ws_bytes, err, stream),
-                "tq_paged_decode",
+                L.tq_paged_decode_write(op, C, qp, row3, qp + 4 * C, row3, qp + 8 * C, row3, pp, nb, n_layer,
+                                        n_head, bs, d, layer, self.decode_block_tables.data_ptr(), self._nbd,
+                                        self._nbd, self.decode_context_lens.data_ptr(), Bd, self.decode_max_ctx,
+                                        scale, self.partition_tokens, self._workspace.data_ptr(), self._ws_bytes,
+                                        err, stream),
+                "tq_paged_decode_write",
             )  # fmt: skip
         if self.num_prefill:
+            off = Bd * row3 * 4  # bytes to the first prefill row of qkv
+            _lib.check(
+                L.tq_cache_write(pp, nb, n_layer, n_head, bs, d, layer, qp + off + 4 * C, row3, qp + off + 8 * C,
+                                 row3, self.slot_mapping.data_ptr() + 8 * Bd, N - Bd, err, stream),
+                "tq_cache_write",
+            )  # fmt: skip
             if PagedBatch.launch_hook is not None:
                 PagedBatch.launch_hook(self, "prefill")
             _lib.check(

@@ -102,8 +102,14 @@ def paged_decode(
     partition_tokens: int = 0,
     workspace: torch.Tensor | None = None,
     d_error: torch.Tensor | None = None,
+    k_new: torch.Tensor | None = None,
+    v_new: torch.Tensor | None = None,
 ) -> None:
-    """``out[b] = attention(q[b], keys/values 0..context_lens[b]-1 of sequence b)`` read in place."""
+    """``out[b] = attention(q[b], keys/values 0..context_lens[b]-1 of sequence b)`` read in place.
+
+    With ``k_new`` / ``v_new`` (rows like ``q``), row b's new K/V are first written into the
+    slot of position ``context_lens[b] - 1`` (``tq_paged_decode_write``): the cache write of the
+    one new token per sequence folded into the same launch."""
     nb, n_layer, n_head, bs, d = _pool_dims(pool)
     if not 0 <= layer < n_layer:
         raise ValueError(f"layer {layer} out of range [0, {n_layer})")
@@ -124,13 +130,20 @@ def paged_decode(
         ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     err = d_error.data_ptr() if d_error is not None else None
     bt_stride = block_tables.stride(0) if n > 1 else block_tables.size(1)
-    st = _lib.lib().tq_paged_decode(
-        out.data_ptr(), os_, q.data_ptr(), qs, pool.data_ptr(), nb, n_layer, n_head, bs, d, layer,
-        block_tables.data_ptr(), bt_stride, block_tables.size(1),
-        context_lens.data_ptr(), n, int(max_context_len), scale, partition_tokens,
-        ws_ptr, ws_bytes, err, _stream(pool.device),
-    )  # fmt: skip
-    _lib.check(st, "tq_paged_decode")
+    tail = (pool.data_ptr(), nb, n_layer, n_head, bs, d, layer, block_tables.data_ptr(), bt_stride,
+            block_tables.size(1), context_lens.data_ptr(), n, int(max_context_len), scale, partition_tokens,
+            ws_ptr, ws_bytes, err, _stream(pool.device))  # fmt: skip
+    if k_new is None and v_new is None:
+        st = _lib.lib().tq_paged_decode(out.data_ptr(), os_, q.data_ptr(), qs, *tail)
+        _lib.check(st, "tq_paged_decode")
+        return
+    if k_new is None or v_new is None:
+        raise ValueError("k_new and v_new go together")
+    ks = _rows(k_new, "k_new", n, n_head, pool.device)
+    vs = _rows(v_new, "v_new", n, n_head, pool.device)
+    st = _lib.lib().tq_paged_decode_write(out.data_ptr(), os_, q.data_ptr(), qs, k_new.data_ptr(), ks,
+                                          v_new.data_ptr(), vs, *tail)  # fmt: skip
+    _lib.check(st, "tq_paged_decode_write")
 
 
 def paged_prefill(
