@@ -36,9 +36,9 @@ MFMA_FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix
 N_SEQS, CTX_LO, CTX_HI, BLOCK, POOL_BLOCKS = 256, 256, 1024, 16, 16384
 # HBM bytes the decode kernel moves per algorithmic byte on this workload, from two rocprofv3
 # counter runs on ``bench.py --pmc-probe`` (FETCH_SIZE scaled x2.0 and WRITE_SIZE x1.0, the factors
-# a 1 GiB copy kernel of known size gives): 960.0 MB read + 0.79 MB written per launch for
-# 949.4 MB algorithmic. The excess is the masked tail of each sequence's last 16-position chunk.
-DECODE_TRAFFIC_PER_ALGO_BYTE = 1.0121
+# a 1 GiB copy kernel of known size gives): 933.56 MB read + 2.36 MB written per launch for
+# 921.04 MB algorithmic. The excess is the masked tail of each sequence's last 16-position chunk.
+DECODE_TRAFFIC_PER_ALGO_BYTE = 1.0162
 
 
 def log(msg: str) -> None:
@@ -404,7 +404,7 @@ def main() -> int:
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": int(bytes_per_launch * DECODE_TRAFFIC_PER_ALGO_BYTE),
             "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on bench.py --pmc-probe, "
-            "scaled by a 1 GiB copy calibration: 1.0121 x algorithmic bytes",
+            "scaled by a 1 GiB copy calibration: 1.0162 x algorithmic bytes",
             "kernel_us": round(kern_ms * 1e3, 2),
             "bytes_per_launch": int(bytes_per_launch),
             "launches": n_launch,
