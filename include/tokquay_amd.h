@@ -9,9 +9,10 @@
  *   tq_paged_decode_write  the same, with the new token's cache write folded in
  *   tq_paged_prefill  causal (chunked) prefill attention straight off the pool
  *
- * plus the greedy-sampling reduction that ends a decode step:
+ * plus two kernels of the model step around them:
  *
- *   tq_argmax_rows    index of each logit row's maximum
+ *   tq_argmax_rows    index of each logit row's maximum (greedy sampling)
+ *   tq_add_layernorm  residual add fused with the LayerNorm that follows it
  *
  * KV pool layout (identical to the reference's, bit for bit):
  *
@@ -60,11 +61,12 @@ typedef enum tq_status {
 #define TQ_DEVERR_BLOCK_ID 1   /* a block-table entry outside [0, num_blocks) */
 #define TQ_DEVERR_SLOT 2       /* a slot_mapping entry >= num_blocks * block_size */
 #define TQ_DEVERR_LENGTH 4     /* a context / query length the block table cannot hold */
+#define TQ_DEVERR_ORDER 8      /* a seq_order entry outside [0, num_seqs) */
 
 /* Human-readable name of a status code (static storage, never NULL). */
 const char* tq_status_string(tq_status status);
 
-/* Version of this ABI; bumped whenever a signature changes. */
+/* Version of this ABI; bumped whenever a signature changes (2: seq_order in the decode entry points). */
 int32_t tq_abi_version(void);
 
 /* Message of the last TQ_ERR_HIP on the calling thread ("" if none). */
@@ -110,6 +112,12 @@ tq_status tq_cache_write(float* pool, int64_t num_blocks, int32_t num_layers, in
  * out + b * out_row_stride. Rows with context_lens[b] == 0 get zeros.
  * max_context_len must be >= every context_lens[b] (it sizes the grid).
  *
+ * seq_order (may be NULL) is the order the sequences' workgroups are dispatched
+ * in: a permutation of 0..num_seqs-1 (entries outside that range are reported
+ * with TQ_DEVERR_ORDER and skipped). Older waves win arbitration, so listing the
+ * longest contexts first shortens the launch's tail (-7 % on 256 sequences of
+ * U[256,1024] positions). NULL is the natural order.
+ *
  * The kernel splits each sequence into partitions of partition_tokens
  * positions (a multiple of 16, at most 1024; 0 = choose automatically) and merges them with
  * a log-sum-exp pass when a sequence spans several. The merge needs
@@ -125,7 +133,8 @@ tq_status tq_paged_decode(float* out, int64_t out_row_stride,
                           int32_t num_heads, int32_t block_size, int32_t head_dim, int32_t layer,
                           const int32_t* block_tables, int64_t block_table_stride,
                           int32_t max_blocks_per_seq,
-                          const int32_t* context_lens, int32_t num_seqs, int32_t max_context_len,
+                          const int32_t* context_lens, const int32_t* seq_order,
+                          int32_t num_seqs, int32_t max_context_len,
                           float scale, int32_t partition_tokens,
                           void* workspace, size_t workspace_bytes,
                           int32_t* d_error, void* stream);
@@ -155,7 +164,8 @@ tq_status tq_paged_decode_write(float* out, int64_t out_row_stride,
                                 int32_t num_heads, int32_t block_size, int32_t head_dim, int32_t layer,
                                 const int32_t* block_tables, int64_t block_table_stride,
                                 int32_t max_blocks_per_seq,
-                                const int32_t* context_lens, int32_t num_seqs, int32_t max_context_len,
+                                const int32_t* context_lens, const int32_t* seq_order,
+                                int32_t num_seqs, int32_t max_context_len,
                                 float scale, int32_t partition_tokens,
                                 void* workspace, size_t workspace_bytes,
                                 int32_t* d_error, void* stream);
@@ -205,6 +215,24 @@ tq_status tq_paged_prefill(float* out, int64_t out_row_stride,
  */
 tq_status tq_argmax_rows(int64_t* out, const float* logits, int64_t num_rows, int64_t num_cols,
                          int64_t row_stride, void* stream);
+
+/*
+ * Residual add + LayerNorm over rows of `cols` fp32 values:
+ *
+ *   s = x[r] + y[r];  x_out[r] = s;  h_out[r] = (s - mean(s)) / sqrt(var(s) + eps) * gamma + beta
+ *
+ * (biased variance, as torch's LayerNorm). Row r of each matrix starts at
+ * ptr + r * stride (elements). cols a multiple of 4, at most 2048; pointers and
+ * strides 16-byte aligned. Outputs may alias inputs element for element
+ * (x_out == x is the in-place residual update).
+ *
+ * Replaces the residual adds of Block.forward (tokquay/model.py:122-123) with
+ * the LayerNorm that follows each (ln_2, the next block's ln_1, ln_f at :180).
+ */
+tq_status tq_add_layernorm(float* x_out, int64_t x_out_stride, float* h_out, int64_t h_out_stride,
+                           const float* x, int64_t x_stride, const float* y, int64_t y_stride,
+                           const float* gamma, const float* beta, int64_t rows, int32_t cols,
+                           float eps, void* stream);
 
 #ifdef __cplusplus
 }

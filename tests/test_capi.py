@@ -47,7 +47,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_status_strings_and_version(lib):
-    assert lib.tq_abi_version() == 1
+    assert lib.tq_abi_version() == 2
     assert lib.tq_status_string(0) == b"ok"
     assert lib.tq_status_string(3) == b"workspace missing or too small"
     assert lib.tq_last_hip_error() == b""
@@ -63,20 +63,20 @@ def test_invalid_arguments_are_rejected_before_any_launch(lib):
     # zero tokens is a no-op
     assert lib.tq_cache_write(None, 8, 2, 12, 16, 64, 0, None, 768, None, 768, None, 0, None, None) == 0
     # decode: null pointers with sequences to do
-    assert lib.tq_paged_decode(None, 768, None, 768, None, 8, 1, 12, 16, 64, 0, None, 4, 4, None, 2, 64,
+    assert lib.tq_paged_decode(None, 768, None, 768, None, 8, 1, 12, 16, 64, 0, None, 4, 4, None, None, 2, 64,
                                0.125, 0, None, 0, None, None) == 1  # fmt: skip
     # decode: partition not a multiple of 16
-    assert lib.tq_paged_decode(None, 768, None, 768, None, 8, 1, 12, 16, 64, 0, None, 4, 4, None, 2, 64,
+    assert lib.tq_paged_decode(None, 768, None, 768, None, 8, 1, 12, 16, 64, 0, None, 4, 4, None, None, 2, 64,
                                0.125, 24, None, 0, None, None) == 1  # fmt: skip
     # decode with the write folded in: null new rows with sequences to do
     assert lib.tq_paged_decode_write(None, 768, None, 2304, None, 2304, None, 2304, None, 8, 1, 12, 16, 64, 0,
-                                     None, 4, 4, None, 2, 64, 0.125, 0, None, 0, None, None) == 1  # fmt: skip
+                                     None, 4, 4, None, None, 2, 64, 0.125, 0, None, 0, None, None) == 1  # fmt: skip
     # ... new-row stride shorter than a row of heads
     assert lib.tq_paged_decode_write(None, 768, None, 2304, 16, 700, 16, 2304, None, 8, 1, 12, 16, 64, 0,
-                                     None, 4, 4, None, 2, 64, 0.125, 0, None, 0, None, None) == 1  # fmt: skip
+                                     None, 4, 4, None, None, 2, 64, 0.125, 0, None, 0, None, None) == 1  # fmt: skip
     # ... zero sequences is a no-op
     assert lib.tq_paged_decode_write(None, 768, None, 2304, None, 2304, None, 2304, None, 8, 1, 12, 16, 64, 0,
-                                     None, 4, 4, None, 0, 64, 0.125, 0, None, 0, None, None) == 0  # fmt: skip
+                                     None, 4, 4, None, None, 0, 64, 0.125, 0, None, 0, None, None) == 0  # fmt: skip
     # prefill: zero sequences is a no-op
     assert lib.tq_paged_prefill(None, 768, None, 768, None, 8, 1, 12, 16, 64, 0, None, 4, 4, None, None,
                                 0, 0, 0, 0.125, None, None) == 0  # fmt: skip

@@ -103,6 +103,42 @@ def test_decode_write_equals_cache_write_then_decode(block_size, partition_token
     assert not torch.equal(pb, pool0.cuda())  # the new rows did land
 
 
+def test_decode_dispatch_order_does_not_change_results():
+    """seq_order only reorders the dispatch: identical bits for any permutation; an entry out of range
+    is reported (TQ_DEVERR_ORDER) and skipped."""
+    from tokquay_amd import _lib, ops
+
+    rng = random.Random(12)
+    ctx = [rng.randint(1, 700) for _ in range(40)]
+    nb = sum(cdiv(c, 16) for c in ctx) + 4
+    pool = torch.randn(nb, 1, 2, 12, 16, 64, generator=torch.Generator().manual_seed(12)).cuda()
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(13)).tolist()
+    width = max(cdiv(c, 16) for c in ctx)
+    tables = torch.zeros(len(ctx), width, dtype=torch.int32)
+    i = 0
+    for b, c in enumerate(ctx):
+        tables[b, : cdiv(c, 16)] = torch.tensor(perm[i : i + cdiv(c, 16)], dtype=torch.int32)
+        i += cdiv(c, 16)
+    tables, cl = tables.cuda(), torch.tensor(ctx, dtype=torch.int32, device="cuda")
+    q = torch.randn(len(ctx), 768, generator=torch.Generator().manual_seed(14)).cuda()
+    outs = []
+    for order in (None, sorted(range(len(ctx)), key=lambda b: -ctx[b]), torch.randperm(len(ctx)).tolist()):
+        out = torch.empty_like(q)
+        so = None if order is None else torch.tensor(order, dtype=torch.int32, device="cuda")
+        ops.paged_decode(out, q, pool, 0, tables, cl, max(ctx), partition_tokens=64, seq_order=so)
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    bad = torch.arange(len(ctx), dtype=torch.int32, device="cuda")
+    bad[3] = len(ctx) + 7
+    out = torch.zeros_like(q)
+    ops.paged_decode(out, q, pool, 0, tables, cl, max(ctx), seq_order=bad, d_error=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == _lib.DEVERR_ORDER
+    keep = [b for b in range(len(ctx)) if b != 3]
+    assert torch.equal(out[keep], outs[0][keep])
+
+
 def test_decode_config4_scale():
     """256 sequences, contexts ~ U[256, 1024], block size 16 (the decode-throughput workload's shape)."""
     rng = random.Random(4)

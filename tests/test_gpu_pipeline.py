@@ -189,3 +189,37 @@ def test_pipelined_engine_eos_and_abort_match_synchronous_engine(model):
             assert long_[: len(short)] == short and len(long_) - len(short) <= 1
         else:
             assert a == b, i
+
+
+# ------------------------------------------------------------------------------ add + LayerNorm
+@pytest.mark.parametrize("rows,cols", [(1, 768), (256, 768), (37, 64), (5, 2048), (3, 4), (9, 1028)])
+def test_add_layernorm_matches_torch(rows, cols):
+    """tq_add_layernorm == (x + y, F.layer_norm(x + y)) in fp32 (torch on the CPU as the reference)."""
+    g = torch.Generator().manual_seed(rows * 31 + cols)
+    x = torch.randn(rows, cols, generator=g) * 3 + 1
+    y = torch.randn(rows, cols, generator=g)
+    w = torch.randn(cols, generator=g)
+    b = torch.randn(cols, generator=g)
+    s_ref = x + y
+    h_ref = torch.nn.functional.layer_norm(s_ref, (cols,), w, b, 1e-5)
+    s, h = ops.add_layernorm(x.cuda(), y.cuda(), w.cuda(), b.cuda(), 1e-5)
+    assert torch.equal(s.cpu(), s_ref)  # one fp32 add per element: exact
+    torch.testing.assert_close(h.cpu(), h_ref, rtol=1e-5, atol=1e-5)
+
+
+def test_add_layernorm_in_place_and_strided_views():
+    g = torch.Generator().manual_seed(3)
+    big = torch.randn(16, 2 * 768, generator=g).cuda()
+    y = big[:, 768:]  # rows 1536 apart
+    x = torch.randn(16, 768, generator=g).cuda()
+    w, b = torch.randn(768, generator=g).cuda(), torch.randn(768, generator=g).cuda()
+    want_s = (x + y).cpu()
+    want_h = torch.nn.functional.layer_norm(want_s, (768,), w.cpu(), b.cpu(), 1e-5)
+    out, h = ops.add_layernorm(x, y, w, b, 1e-5, x_out=x)
+    assert out.data_ptr() == x.data_ptr()
+    assert torch.equal(x.cpu(), want_s)
+    torch.testing.assert_close(h.cpu(), want_h, rtol=1e-5, atol=1e-5)
+    from tokquay_amd import _lib
+
+    with pytest.raises(_lib.KernelError):
+        ops.add_layernorm(x[:, :766], y[:, :766], w[:766], b[:766], 1e-5)  # 766 columns: not a multiple of 4

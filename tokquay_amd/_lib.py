@@ -21,6 +21,7 @@ STATUS_NAMES = {0: "ok", 1: "invalid argument", 2: "unsupported shape", 3: "work
 DEVERR_BLOCK_ID = 1
 DEVERR_SLOT = 2
 DEVERR_LENGTH = 4
+DEVERR_ORDER = 8
 
 # name -> (restype, argtypes); the order of argtypes is the C declaration's.
 SIGNATURES: dict[str, tuple] = {
@@ -47,7 +48,7 @@ SIGNATURES: dict[str, tuple] = {
             c_f32p, ctypes.c_int64, ctypes.c_int32,  # pool, num_blocks, num_layers
             ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,  # num_heads, block_size, head_dim, layer
             c_i32p, ctypes.c_int64, ctypes.c_int32,  # block_tables, block_table_stride, max_blocks_per_seq
-            c_i32p, ctypes.c_int32, ctypes.c_int32,  # context_lens, num_seqs, max_context_len
+            c_i32p, c_i32p, ctypes.c_int32, ctypes.c_int32,  # context_lens, seq_order, num_seqs, max_context_len
             ctypes.c_float, ctypes.c_int32,  # scale, partition_tokens
             ctypes.c_void_p, ctypes.c_size_t,  # workspace, workspace_bytes
             c_i32p, ctypes.c_void_p,  # d_error, stream
@@ -63,7 +64,7 @@ SIGNATURES: dict[str, tuple] = {
             c_f32p, ctypes.c_int64, ctypes.c_int32,  # pool, num_blocks, num_layers
             ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,  # num_heads, block_size, head_dim, layer
             c_i32p, ctypes.c_int64, ctypes.c_int32,  # block_tables, block_table_stride, max_blocks_per_seq
-            c_i32p, ctypes.c_int32, ctypes.c_int32,  # context_lens, num_seqs, max_context_len
+            c_i32p, c_i32p, ctypes.c_int32, ctypes.c_int32,  # context_lens, seq_order, num_seqs, max_context_len
             ctypes.c_float, ctypes.c_int32,  # scale, partition_tokens
             ctypes.c_void_p, ctypes.c_size_t,  # workspace, workspace_bytes
             c_i32p, ctypes.c_void_p,  # d_error, stream
@@ -84,6 +85,14 @@ SIGNATURES: dict[str, tuple] = {
             c_i32p, c_i32p,  # cu_seqlens_q, q_start
             ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,  # num_seqs, num_q_rows, max_query_len
             ctypes.c_float, c_i32p, ctypes.c_void_p,  # scale, d_error, stream
+        ],
+    ),
+    "tq_add_layernorm": (
+        ctypes.c_int,
+        [
+            c_f32p, ctypes.c_int64, c_f32p, ctypes.c_int64,  # x_out, stride, h_out, stride
+            c_f32p, ctypes.c_int64, c_f32p, ctypes.c_int64,  # x, stride, y, stride
+            c_f32p, c_f32p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float, ctypes.c_void_p,  # gamma, beta, rows, cols, eps, stream
         ],
     ),
     "tq_argmax_rows": (

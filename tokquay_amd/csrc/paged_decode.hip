@@ -60,6 +60,8 @@ struct DecodeArgs {
   const int32_t* block_tables;
   int64_t bt_stride;
   const int32_t* context_lens;
+  const int32_t* seq_order;  // dispatch order of the sequences (nullptr: 0, 1, 2, ...)
+  int32_t num_seqs;
   float* partials;  // [num_seqs][num_heads][max_parts][kPartialStride]
   int32_t* d_error;
   float* pool_layer_w;  // the write variant: writable alias of pool_layer
@@ -259,8 +261,17 @@ __global__ __launch_bounds__(kWave* kHeadsPerGroup) void decode_partition_kernel
   const int lane = threadIdx.x & (kWave - 1);
   const int h = blockIdx.x * kHeadsPerGroup + (threadIdx.x / kWave);
   const int part = blockIdx.y;
-  const int b = blockIdx.z;
   if (h >= a.num_heads) return;  // whole wave leaves; the kernel has no barriers
+  // Workgroups are dispatched in grid order and older waves win arbitration, so a caller
+  // that lists the longest contexts first shortens the tail of the launch.
+  int b = blockIdx.z;
+  if (a.seq_order != nullptr) {
+    b = a.seq_order[blockIdx.z];
+    if ((uint32_t)b >= (uint32_t)a.num_seqs) {
+      if (h == 0 && part == 0 && lane == 0) flag_error(a.d_error, TQ_DEVERR_ORDER);
+      return;
+    }
+  }
   const int bs = BS_CT > 0 ? BS_CT : a.block_size;
   const int ctx = load_context(a, b, part == 0 && h == 0 && lane == 0);
   float* out_row = a.out + (int64_t)b * a.out_stride + h * kHeadDim;
@@ -435,9 +446,9 @@ tq_status paged_decode_impl(float* out, int64_t out_row_stride, const float* q, 
                             int64_t v_new_row_stride, float* pool_w, const float* pool, int64_t num_blocks,
                             int32_t num_layers, int32_t num_heads, int32_t block_size, int32_t head_dim,
                             int32_t layer, const int32_t* block_tables, int64_t block_table_stride,
-                            int32_t max_blocks_per_seq, const int32_t* context_lens, int32_t num_seqs,
-                            int32_t max_context_len, float scale, int32_t partition_tokens, void* workspace,
-                            size_t workspace_bytes, int32_t* d_error, void* stream) {
+                            int32_t max_blocks_per_seq, const int32_t* context_lens, const int32_t* seq_order,
+                            int32_t num_seqs, int32_t max_context_len, float scale, int32_t partition_tokens,
+                            void* workspace, size_t workspace_bytes, int32_t* d_error, void* stream) {
   // Timing events apply to this call only, whatever it returns.
   const TimingEvents timing = take_timing_events();
   hipEvent_t t_start = timing.start, t_stop = timing.stop;
@@ -483,6 +494,8 @@ tq_status paged_decode_impl(float* out, int64_t out_row_stride, const float* q, 
   a.block_tables = block_tables;
   a.bt_stride = block_table_stride;
   a.context_lens = context_lens;
+  a.seq_order = seq_order;
+  a.num_seqs = num_seqs;
   a.partials = static_cast<float*>(workspace);
   a.d_error = d_error;
   a.scale = scale;
@@ -526,14 +539,15 @@ extern "C" tq_status tq_paged_decode(float* out, int64_t out_row_stride, const f
                                      int32_t num_layers, int32_t num_heads, int32_t block_size,
                                      int32_t head_dim, int32_t layer, const int32_t* block_tables,
                                      int64_t block_table_stride, int32_t max_blocks_per_seq,
-                                     const int32_t* context_lens, int32_t num_seqs,
+                                     const int32_t* context_lens, const int32_t* seq_order, int32_t num_seqs,
                                      int32_t max_context_len, float scale, int32_t partition_tokens,
                                      void* workspace, size_t workspace_bytes, int32_t* d_error,
                                      void* stream) {
   return tq::paged_decode_impl(out, out_row_stride, q, q_row_stride, nullptr, 0, nullptr, 0, nullptr, pool,
                                num_blocks, num_layers, num_heads, block_size, head_dim, layer, block_tables,
-                               block_table_stride, max_blocks_per_seq, context_lens, num_seqs, max_context_len,
-                               scale, partition_tokens, workspace, workspace_bytes, d_error, stream);
+                               block_table_stride, max_blocks_per_seq, context_lens, seq_order, num_seqs,
+                               max_context_len, scale, partition_tokens, workspace, workspace_bytes, d_error,
+                               stream);
 }
 
 extern "C" tq_status tq_paged_decode_write(float* out, int64_t out_row_stride, const float* q,
@@ -543,7 +557,8 @@ extern "C" tq_status tq_paged_decode_write(float* out, int64_t out_row_stride, c
                                            int32_t block_size, int32_t head_dim, int32_t layer,
                                            const int32_t* block_tables, int64_t block_table_stride,
                                            int32_t max_blocks_per_seq, const int32_t* context_lens,
-                                           int32_t num_seqs, int32_t max_context_len, float scale,
+                                           const int32_t* seq_order, int32_t num_seqs,
+                                           int32_t max_context_len, float scale,
                                            int32_t partition_tokens, void* workspace, size_t workspace_bytes,
                                            int32_t* d_error, void* stream) {
   using namespace tq;
@@ -562,7 +577,7 @@ extern "C" tq_status tq_paged_decode_write(float* out, int64_t out_row_stride, c
   return paged_decode_impl(out, out_row_stride, q, q_row_stride, num_seqs > 0 ? k_new : nullptr,
                            k_new_row_stride, v_new, v_new_row_stride, pool, pool, num_blocks, num_layers,
                            num_heads, block_size, head_dim, layer, block_tables, block_table_stride,
-                           max_blocks_per_seq, context_lens, num_seqs, max_context_len, scale, partition_tokens,
-                           workspace, workspace_bytes, d_error, stream);
+                           max_blocks_per_seq, context_lens, seq_order, num_seqs, max_context_len, scale,
+                           partition_tokens, workspace, workspace_bytes, d_error, stream);
 }
 

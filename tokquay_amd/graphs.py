@@ -53,14 +53,16 @@ class StaticDecodeBatch:
         dev = pool.device
         cap, mb = capacity, self.max_blocks
         self.d64 = torch.zeros(3 * cap, dtype=torch.int64, device=dev)  # ids | positions | source rows
-        self.d32 = torch.zeros(cap * mb + cap, dtype=torch.int32, device=dev)  # tables | context lengths
+        # tables | context lengths | dispatch order (rows by decreasing context)
+        self.d32 = torch.zeros(cap * mb + 2 * cap, dtype=torch.int32, device=dev)
         self.h64 = torch.zeros(3 * cap, dtype=torch.int64, pin_memory=True)
-        self.h32 = torch.zeros(cap * mb + cap, dtype=torch.int32, pin_memory=True)
+        self.h32 = torch.zeros(cap * mb + 2 * cap, dtype=torch.int32, pin_memory=True)
         self.copied = torch.cuda.Event()
         self.ids, self.positions, self.src = self.d64[:cap], self.d64[cap : 2 * cap], self.d64[2 * cap :]
         self.tokens = torch.zeros(cap, dtype=torch.int64, device=dev)  # greedy ids of the latest replay
         self.tables = self.d32[: cap * mb].view(cap, mb)
-        self.context_lens = self.d32[cap * mb :]
+        self.context_lens = self.d32[cap * mb : cap * mb + cap]
+        self.order = self.d32[cap * mb + cap :]
         n_head = pool.shape[3]
         L = _lib.lib()
         ws = max(int(L.tq_paged_decode_workspace_size(b, n_head, HEAD_DIM, n_positions, 0))
@@ -126,6 +128,8 @@ class StaticDecodeBatch:
         a64[cap + n : cap + bucket] = 0
         tables[n:bucket] = 0
         a32[cap * mb + n : cap * mb + bucket] = 0  # padded rows write and attend to nothing
+        ctx = a32[cap * mb : cap * mb + bucket]
+        a32[cap * mb + cap : cap * mb + cap + bucket] = np.argsort(-ctx, kind="stable")  # longest first
         self.d64.copy_(self.h64, non_blocking=True)
         self.d32.copy_(self.h32, non_blocking=True)
         self.copied.record()
@@ -153,7 +157,7 @@ class StaticDecodeView:
         _lib.check(
             L.tq_paged_decode_write(out.data_ptr(), C, qp, 3 * C, qp + 4 * C, 3 * C, qp + 8 * C, 3 * C, pp, nb,
                                     n_layer, n_head, bs, d, layer, s.tables.data_ptr(), s.max_blocks, s.max_blocks,
-                                    s.context_lens.data_ptr(), n, s.max_ctx, 1.0 / math.sqrt(d), 0,
+                                    s.context_lens.data_ptr(), s.order.data_ptr(), n, s.max_ctx, 1.0 / math.sqrt(d), 0,
                                     s.workspace.data_ptr(), s.workspace.numel(), err, stream),
             "tq_paged_decode_write",
         )  # fmt: skip
@@ -177,10 +181,7 @@ class DecodeGraphs:
         view = s.view(rows)
         src = s.src[:rows]
         ids = torch.where(src >= 0, s.tokens.index_select(0, src.clamp(min=0)), s.ids[:rows])
-        x = m.wte(ids) + m.wpe(s.positions[:rows])
-        for i, block in enumerate(m.h):
-            x = block(x, view, i)
-        logits = m.ln_f(x) @ m.wte.weight.T
+        logits = m.trunk(ids, s.positions[:rows], view) @ m.wte.weight.T
         ops.argmax_rows(logits, out=s.tokens[:rows])
         return logits
 

@@ -238,13 +238,15 @@ class PagedBatch(BatchedKV):
         a64 = h64.numpy()
         tok_idx, pos, slots, last = a64[:N], a64[N : 2 * N], a64[2 * N : 3 * N], a64[3 * N :]
         # int32 metadata: dec_tables[Bd, nbd] | dec_ctx[Bd] | pre_tables[Bp, nbp] | pre_cu[Bp + 1] | pre_start[Bp]
-        n32 = Bd * nbd + Bd + Bp * nbp + (Bp + 1) + Bp
+        # | dec_order[Bd] (decode rows, longest context first: the decode kernel's dispatch order)
+        n32 = Bd * nbd + Bd + Bp * nbp + (Bp + 1) + Bp + Bd
         h32 = torch.zeros(n32, dtype=torch.int32, pin_memory=pin)
         a32 = h32.numpy()
         o_dt, o_dc = 0, Bd * nbd
         o_pt = o_dc + Bd
         o_pc = o_pt + Bp * nbp
         o_ps = o_pc + Bp + 1
+        o_do = o_ps + Bp
         dec_tables = a32[o_dt:o_dc].reshape(Bd, nbd)
         pre_tables = a32[o_pt:o_pc].reshape(Bp, nbp)
 
@@ -272,6 +274,7 @@ class PagedBatch(BatchedKV):
             a32[o_ps + i] = s
             row += n
         a32[o_pc + Bp] = N - Bd
+        a32[o_do:] = np.argsort(-a32[o_dc:o_pt], kind="stable")
 
         d64 = h64.to(device, non_blocking=True)
         d32 = h32.to(device, non_blocking=True)
@@ -283,7 +286,8 @@ class PagedBatch(BatchedKV):
         self.decode_context_lens = d32[o_dc:o_pt]
         self.prefill_block_tables = d32[o_pt:o_pc].view(Bp, nbp)
         self.prefill_cu_seqlens = d32[o_pc:o_ps]
-        self.prefill_start = d32[o_ps:]
+        self.prefill_start = d32[o_ps:o_do]
+        self.decode_order = d32[o_do:]
         self._workspace: torch.Tensor | None = None
         self._ws_bytes = 0
         self._lazy: dict[str, torch.Tensor] = {}
@@ -373,7 +377,8 @@ class PagedBatch(BatchedKV):
             _lib.check(
                 L.tq_paged_decode_write(op, C, qp, row3, qp + 4 * C, row3, qp + 8 * C, row3, pp, nb, n_layer,
                                         n_head, bs, d, layer, self.decode_block_tables.data_ptr(), self._nbd,
-                                        self._nbd, self.decode_context_lens.data_ptr(), Bd, self.decode_max_ctx,
+                                        self._nbd, self.decode_context_lens.data_ptr(), self.decode_order.data_ptr(),
+                                        Bd, self.decode_max_ctx,
                                         scale, self.partition_tokens, self._workspace.data_ptr(), self._ws_bytes,
                                         err, stream),
                 "tq_paged_decode_write",

@@ -22,6 +22,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from tokquay_amd import ops
 from tokquay_amd.kv_cache import PagedBatch
 
 
@@ -68,9 +69,8 @@ class Block(nn.Module):
         self.ln_2 = nn.LayerNorm(cfg.n_embd, eps=cfg.layer_norm_eps)
         self.mlp = MLP(cfg)
 
-    def forward(self, x: torch.Tensor, cache: PagedBatch, layer: int) -> torch.Tensor:
-        x = x + self.attn(self.ln_1(x), cache, layer)
-        return x + self.mlp(self.ln_2(x))
+    # Block.forward of the reference (tokquay/model.py:121-123) is GPT2.trunk's loop body here: each
+    # residual add runs fused with the LayerNorm after it (tq_add_layernorm).
 
 
 class GPT2(nn.Module):
@@ -81,6 +81,23 @@ class GPT2(nn.Module):
         self.wpe = nn.Embedding(self.cfg.n_positions, self.cfg.n_embd)
         self.h = nn.ModuleList(Block(self.cfg) for _ in range(self.cfg.n_layer))
         self.ln_f = nn.LayerNorm(self.cfg.n_embd, eps=self.cfg.layer_norm_eps)
+
+    def trunk(self, ids: torch.Tensor, positions: torch.Tensor, cache) -> torch.Tensor:
+        """Final hidden states ``ln_f(x)`` ``[N, C]`` of packed rows (token ids and positions ``[N]``).
+
+        The reference's loop (tokquay/model.py:172-180): embeddings, ``x = x + attn(ln_1(x))``,
+        ``x = x + mlp(ln_2(x))`` per block, ``ln_f``. Every residual add runs fused with the
+        LayerNorm that follows it (``tq_add_layernorm``); the embedding sum is fused with the
+        first ``ln_1``. ``cache`` provides ``attend(layer, qkv)``."""
+        blocks = self.h
+        first = blocks[0].ln_1
+        x, h = ops.add_layernorm(self.wte(ids), self.wpe(positions), first.weight, first.bias, first.eps)
+        for i, block in enumerate(blocks):
+            a = block.attn(h, cache, i)
+            x, h = ops.add_layernorm(x, a, block.ln_2.weight, block.ln_2.bias, block.ln_2.eps, x_out=x)
+            nxt = blocks[i + 1].ln_1 if i + 1 < len(blocks) else self.ln_f
+            x, h = ops.add_layernorm(x, block.mlp(h), nxt.weight, nxt.bias, nxt.eps, x_out=x)
+        return h
 
     def forward(self, input_ids: torch.Tensor, cache: PagedBatch, last_only: bool = False) -> torch.Tensor:
         """input_ids ``[B, T]`` (new tokens, right-padded) -> logits ``[B, T, vocab]``, or ``[B, 1, vocab]``
@@ -94,13 +111,10 @@ class GPT2(nn.Module):
             raise ValueError(f"sequence length {cache.max_ctx} exceeds n_positions={self.cfg.n_positions}")
 
         ids = input_ids.reshape(-1).index_select(0, cache.token_index)  # [N] real tokens only
-        x = self.wte(ids) + self.wpe(cache.packed_positions)  # positions of real tokens are < n_positions
-        for i, block in enumerate(self.h):
-            x = block(x, cache, i)
+        h = self.trunk(ids, cache.packed_positions, cache)  # positions of real tokens are < n_positions
         if last_only:
-            x = self.ln_f(x.index_select(0, cache.last_rows))  # [B, C]
-            return (x @ self.wte.weight.T)[:, None]  # tied LM head
-        logits = self.ln_f(x) @ self.wte.weight.T  # [N, vocab]
+            return (h.index_select(0, cache.last_rows) @ self.wte.weight.T)[:, None]  # tied LM head, [B, 1, V]
+        logits = h @ self.wte.weight.T  # [N, vocab]
         full = logits.new_zeros(B * T, logits.size(-1))
         full[cache.token_index] = logits
         return full.view(B, T, -1)

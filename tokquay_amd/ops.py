@@ -104,12 +104,14 @@ def paged_decode(
     d_error: torch.Tensor | None = None,
     k_new: torch.Tensor | None = None,
     v_new: torch.Tensor | None = None,
+    seq_order: torch.Tensor | None = None,
 ) -> None:
     """``out[b] = attention(q[b], keys/values 0..context_lens[b]-1 of sequence b)`` read in place.
 
     With ``k_new`` / ``v_new`` (rows like ``q``), row b's new K/V are first written into the
     slot of position ``context_lens[b] - 1`` (``tq_paged_decode_write``): the cache write of the
-    one new token per sequence folded into the same launch."""
+    one new token per sequence folded into the same launch. ``seq_order`` (int32 ``[B]``, a
+    permutation) is the order the sequences are dispatched in; longest contexts first is fastest."""
     nb, n_layer, n_head, bs, d = _pool_dims(pool)
     if not 0 <= layer < n_layer:
         raise ValueError(f"layer {layer} out of range [0, {n_layer})")
@@ -130,8 +132,14 @@ def paged_decode(
         ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     err = d_error.data_ptr() if d_error is not None else None
     bt_stride = block_tables.stride(0) if n > 1 else block_tables.size(1)
+    order = None
+    if seq_order is not None:
+        _int_tensor(seq_order, "seq_order", torch.int32, pool.device)
+        if seq_order.numel() != n:
+            raise ValueError(f"seq_order needs {n} entries")
+        order = seq_order.data_ptr()
     tail = (pool.data_ptr(), nb, n_layer, n_head, bs, d, layer, block_tables.data_ptr(), bt_stride,
-            block_tables.size(1), context_lens.data_ptr(), n, int(max_context_len), scale, partition_tokens,
+            block_tables.size(1), context_lens.data_ptr(), order, n, int(max_context_len), scale, partition_tokens,
             ws_ptr, ws_bytes, err, _stream(pool.device))  # fmt: skip
     if k_new is None and v_new is None:
         st = _lib.lib().tq_paged_decode(out.data_ptr(), os_, q.data_ptr(), qs, *tail)
@@ -207,3 +215,30 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.
     st = _lib.lib().tq_argmax_rows(out.data_ptr(), logits.data_ptr(), rows, cols, stride, _stream(logits.device))
     _lib.check(st, "tq_argmax_rows")
     return out
+
+
+def add_layernorm(x: torch.Tensor, y: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float,
+                  x_out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(x + y, layer_norm(x + y))`` for float32 rows ``[R, C]`` in one pass (``tq_add_layernorm``): a
+    residual add of Block.forward (tokquay/model.py:122-123) and the LayerNorm after it. ``x_out``
+    (default: a new tensor) may be ``x`` itself for an in-place residual update."""
+    if x.dim() != 2 or y.shape != x.shape or not x.is_cuda:
+        raise ValueError("x and y must be [rows, cols] tensors of one shape on a HIP device")
+    rows, cols = x.shape
+    for name, t in (("x", x), ("y", y)):
+        if t.dtype != torch.float32 or t.device != x.device or t.stride(1) != 1:
+            raise ValueError(f"{name} must be float32 with contiguous rows on {x.device}")
+    for name, t in (("weight", weight), ("bias", bias)):
+        if t.dtype != torch.float32 or t.device != x.device or t.shape != (cols,) or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous float32 [{cols}] tensor on {x.device}")
+    if x_out is None:
+        x_out = torch.empty_like(x, memory_format=torch.contiguous_format)
+    elif x_out.shape != x.shape or x_out.dtype != torch.float32 or x_out.stride(1) != 1 or x_out.device != x.device:
+        raise ValueError("x_out must be a float32 tensor shaped like x with contiguous rows")
+    h = torch.empty(rows, cols, dtype=torch.float32, device=x.device)
+    stride = lambda t: t.stride(0) if rows > 1 else cols  # noqa: E731  (a one-row view may carry any stride)
+    st = _lib.lib().tq_add_layernorm(x_out.data_ptr(), stride(x_out), h.data_ptr(), cols, x.data_ptr(), stride(x),
+                                     y.data_ptr(), stride(y), weight.data_ptr(), bias.data_ptr(), rows, cols,
+                                     float(eps), _stream(x.device))  # fmt: skip
+    _lib.check(st, "tq_add_layernorm")
+    return x_out, h
