@@ -148,7 +148,7 @@ def test_decode_config4_scale():
 
 
 # ------------------------------------------------------------------------------ prefill
-@pytest.mark.parametrize("block_size", [4, 16])
+@pytest.mark.parametrize("block_size", [4, 16, 32, 48])
 @pytest.mark.parametrize("start,n", [(0, 2), (0, 15), (0, 16), (0, 17), (0, 100), (5, 40), (16, 16), (250, 300), (0, 1024)])
 def test_prefill_single_sequence(block_size, start, n):
     sc = Scenario([start], [n], block_size=block_size, seed=start * 7 + n)
@@ -270,12 +270,15 @@ def test_launch_recorded_timing_events():
     assert torch.equal(got, want)
 
 
-@pytest.mark.parametrize("num_seqs", [24, 12, 6, 2])  # 4608 / 2304 / 1152 / 384 query tiles: key split 1 / 2 / 4 / 8
-def test_prefill_key_split_widths(num_seqs):
+@pytest.mark.parametrize("block_size", [8, 16])
+@pytest.mark.parametrize("num_seqs", [24, 12, 6, 2])
+def test_prefill_key_split_widths(block_size, num_seqs):
     """The prefill launch splits each query tile's keys over 1, 2, 4 or 8 waves depending on how many
-    tiles there are; every width must match the reference, with ragged lengths and chunk starts."""
+    tiles there are (4608 / 2304 / 1152 / 384 query tiles -> 1 / 2 / 4 / 8 waves), for the
+    block-size-16 path (one block per key tile) and the generic one; every width must match the
+    reference, with ragged lengths and chunk starts."""
     rng = random.Random(num_seqs)
     lens = [256] + [rng.randint(100, 256) for _ in range(num_seqs - 1)]
     starts = [rng.choice([0, 0, 100, 300]) for _ in range(num_seqs)]
-    sc = Scenario(starts, lens, block_size=16, seed=90 + num_seqs)
+    sc = Scenario(starts, lens, block_size=block_size, seed=90 + num_seqs)
     check(sc, brute=num_seqs <= 6)

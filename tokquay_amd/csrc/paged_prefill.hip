@@ -20,7 +20,8 @@
 //
 // Masking is index arithmetic: query i of sequence b sits at q_start[b] + i
 // and sees keys j <= q_start[b] + i (tokquay/kv_cache.py:208-214). Online
-// softmax keeps one running max per query, shared by its four lane groups.
+// softmax keeps one running max per query, shared by its four lane groups
+// (combined with gfx950's cross-row lane swaps, no LDS traffic).
 //
 // Reference semantics: PagedBatch.gather + mask (tokquay/kv_cache.py:208-214,
 // :234-242) and Attention.forward's masked softmax (tokquay/model.py:94-96).
@@ -124,12 +125,37 @@ __device__ __forceinline__ void load_kv_tile(const PrefillArgs& a, const int32_t
   }
 }
 
+// Max of v over the four lanes j, j + 16, j + 32, j + 48 (one query's lane groups), left in all
+// four: gfx950's cross-row lane swaps (v_permlane16_swap / v_permlane32_swap) on the VALU instead
+// of two LDS-unit permutes per key tile.
+__device__ __forceinline__ float max_over_lane_groups(float v) {
+  const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(p16[0]), __uint_as_float(p16[1]));  // rows 0<->1, 2<->3
+  const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(p32[0]), __uint_as_float(p32[1]));  // lanes 0-31 <-> 32-63
+}
+
 // Same loads when a 16-key tile is exactly one block (block size 16): the tile's
 // block id arrives as a wave-uniform scalar (blk < 0: out of range, load zeros).
 __device__ __forceinline__ void load_kv_block_tile(const PrefillArgs& a, const float* head_base, int64_t blk,
                                                    int kt, int kend, int j, int g, float (&kreg)[16],
                                                    float4 (&vreg)[4]) {
   const float* base = head_base + (blk < 0 ? 0 : blk) * a.block_stride;
+  if (blk >= 0 && kt + kTile <= kend) {  // uniform: every key of the tile is valid, nothing to mask
+    const float* kp = base + j * kHeadDim + 16 * g;
+#pragma unroll
+    for (int v4 = 0; v4 < 4; ++v4) {
+      const float4 x = *reinterpret_cast<const float4*>(kp + 4 * v4);
+      kreg[4 * v4 + 0] = x.x;
+      kreg[4 * v4 + 1] = x.y;
+      kreg[4 * v4 + 2] = x.z;
+      kreg[4 * v4 + 3] = x.w;
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      vreg[s] = *reinterpret_cast<const float4*>(base + a.kv_stride + (4 * g + s) * kHeadDim + 4 * j);
+    return;
+  }
   const bool k_ok = blk >= 0 && kt + j < kend;
   const float* kp = base + j * kHeadDim + 16 * g;
 #pragma unroll
@@ -227,10 +253,14 @@ __global__ __launch_bounds__(kWave* KS) void prefill_kernel(const PrefillArgs a)
     } else {
       load_kv_tile<BS_CT>(a, bt, head_base, bs, kt, kend, j, g, kreg, vreg);
     }
-    floatx4 st = {0.f, 0.f, 0.f, 0.f};
+    // Two independent MFMA chains (even / odd dim groups) halve the dependent latency.
+    floatx4 st0 = {0.f, 0.f, 0.f, 0.f}, st1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < 16; ++s) st = __builtin_amdgcn_mfma_f32_16x16x4f32(kreg[s], qreg[s], st, 0, 0, 0);
-    // st[r] = S^T[key kt + 4g + r][query j]
+    for (int s = 0; s < 16; s += 2) {
+      st0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kreg[s], qreg[s], st0, 0, 0, 0);
+      st1 = __builtin_amdgcn_mfma_f32_16x16x4f32(kreg[s + 1], qreg[s + 1], st1, 0, 0, 0);
+    }
+    const floatx4 st = st0 + st1;  // st[r] = S^T[key kt + 4g + r][query j]
 
     float sm[4];
     float tmax = -INFINITY;
@@ -240,8 +270,7 @@ __global__ __launch_bounds__(kWave* KS) void prefill_kernel(const PrefillArgs a)
       sm[r] = key <= qpos ? st[r] : -INFINITY;
       tmax = fmaxf(tmax, sm[r]);
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    tmax = max_over_lane_groups(tmax);
     const float mn = fmaxf(m, tmax);
     // A wave whose tiles start past a query's position has seen no visible key
     // for it yet (mn = -inf): any finite reference keeps its state exactly zero
@@ -331,11 +360,12 @@ void launch_prefill_ks(const PrefillArgs& a, hipStream_t stream, hipEvent_t star
                           stop, 0, a);
 }
 
-// Waves per workgroup: enough (sequence, head, query tile) work items times KS
-// to give every SIMD of the 256 CUs about four waves.
+// Waves per workgroup: double the key split while the (sequence, head, query tile)
+// work items times KS give fewer than three waves per SIMD of the 256 CUs, up to 8
+// (measured on 256-token chunks: 768 tiles run best with 4, 576 tiles with 8).
 int choose_key_split(int64_t tiles) {
   int ks = 1;
-  while (ks < 8 && tiles * ks < 4096) ks *= 2;
+  while (ks < 8 && tiles * ks < 3072) ks *= 2;
   return ks;
 }
 
