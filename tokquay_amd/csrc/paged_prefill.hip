@@ -177,7 +177,9 @@ __device__ __forceinline__ void load_kv_block_tile(const PrefillArgs& a, const f
 template <int BS_CT, int KS>
 __global__ __launch_bounds__(kWave* KS) void prefill_kernel(const PrefillArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  // Wave-uniform by construction; readfirstlane lets the compiler keep the key-tile loop
+  // (counter, bounds, branches) in scalar registers.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   int qt, h, b;
   tile_of(a, qt, h, b);
   const int bs = BS_CT > 0 ? BS_CT : a.block_size;
