@@ -132,3 +132,23 @@ def check(status: int, what: str) -> None:
         if status == 4:
             msg += f": {lib().tq_last_hip_error().decode(errors='replace')}"
         raise KernelError(f"{what} failed: {msg}")
+
+
+_native = None
+
+
+def native():
+    """The ``_native`` extension (metadata builder and per-layer launcher); raises if it was never built."""
+    global _native
+    if _native is None:
+        from tokquay_amd.build import NATIVE_PATH
+
+        if not os.path.exists(NATIVE_PATH):
+            raise RuntimeError(
+                f"{NATIVE_PATH} is missing: build it first (python -m tokquay_amd.build, or __graft_entry__.build())"
+            )
+        lib()  # binds the kernel library the extension links (same file, loaded once)
+        from tokquay_amd import _native as mod
+
+        _native = mod
+    return _native

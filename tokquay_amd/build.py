@@ -1,8 +1,12 @@
-"""Builds ``libtokquay_amd.so`` (the gfx950 kernels and their C ABI) in place.
+"""Builds ``libtokquay_amd.so`` (the gfx950 kernels and their C ABI) in place,
+then the host-only CPython extension ``_native`` that links it.
 
 Run ``python -m tokquay_amd.build``. The library is compiled straight with
 ``hipcc`` for gfx950 only; it has no torch dependency, so any host program can
-load it through ``include/tokquay_amd.h``.
+load it through ``include/tokquay_amd.h``. ``_native`` (the batch view's
+metadata builder and per-layer launcher, ``csrc/native.cpp``) is plain C++
+built with the host compiler against the Python headers; it finds the kernel
+library next to itself (rpath ``$ORIGIN``).
 """
 
 from __future__ import annotations
@@ -11,6 +15,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
@@ -19,6 +24,8 @@ INCLUDE_DIR = os.path.join(REPO_DIR, "include")
 LIB_NAME = "libtokquay_amd.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 OFFLOAD_ARCH = "gfx950"
+NATIVE_SRC = os.path.join(CSRC_DIR, "native.cpp")
+NATIVE_PATH = os.path.join(PKG_DIR, "_native" + sysconfig.get_config_var("EXT_SUFFIX"))
 
 HIPCC_FLAGS = [
     f"--offload-arch={OFFLOAD_ARCH}",
@@ -47,6 +54,13 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = False) -> str:
+    """Compile every kernel source into LIB_PATH, then the ``_native`` extension; return LIB_PATH."""
+    build_kernels(verbose)
+    build_native(verbose)
+    return LIB_PATH
+
+
+def build_kernels(verbose: bool = False) -> str:
     """Compile every kernel source into LIB_PATH and return that path."""
     tmp = LIB_PATH + ".tmp"
     cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", "-o", tmp, *sources()]
@@ -62,6 +76,26 @@ def build(verbose: bool = False) -> str:
         print("\n".join(msgs), flush=True)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
+
+
+def build_native(verbose: bool = False) -> str:
+    """Compile ``csrc/native.cpp`` into the ``_native`` extension (links LIB_PATH) and return its path."""
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if cxx is None:
+        raise RuntimeError("no host C++ compiler (g++) found")
+    tmp = NATIVE_PATH + ".tmp"
+    cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", "-Wno-missing-field-initializers",
+           f"-I{sysconfig.get_paths()['include']}", f"-I{INCLUDE_DIR}", "-o", tmp, NATIVE_SRC,
+           f"-L{PKG_DIR}", "-l:" + LIB_NAME, "-Wl,-rpath,$ORIGIN"]  # fmt: skip
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"{cxx} failed ({proc.returncode}):\n{proc.stdout}{proc.stderr}")
+    if verbose and (proc.stdout or proc.stderr):
+        print(proc.stdout + proc.stderr, flush=True)
+    os.replace(tmp, NATIVE_PATH)
+    return NATIVE_PATH
 
 
 if __name__ == "__main__":

@@ -27,7 +27,6 @@ from __future__ import annotations
 
 import math
 
-import numpy as np
 import torch
 
 from tokquay_amd import _lib, ops
@@ -69,7 +68,6 @@ class StaticDecodeBatch:
                  for b in self.buckets())  # fmt: skip
         self.workspace = torch.empty(max(ws, 16), dtype=torch.uint8, device=dev)
         self.error_word = allocator.error_word
-        self._rows: dict[int, tuple[np.ndarray, int]] = {}  # seq_id -> (padded table row, table length)
 
     def buckets(self) -> list[int]:
         out, b = [], 1
@@ -85,51 +83,14 @@ class StaticDecodeBatch:
         sequence feeds the token the previous replay chose for row ``src_rows[i]``, which
         the host has not appended yet (so the sequence has no uncached token)."""
         self.copied.synchronize()  # the previous step's copy has left the staging buffers
-        cap, mb, bs = self.capacity, self.max_blocks, self.block_size
-        n = len(seqs)
-        pending = 1 if src_rows is None else 0
-        if src_rows is not None and (len(src_rows) != n or (n and not 0 <= min(src_rows) <= max(src_rows) < cap)):
-            raise ValueError(f"src_rows needs one entry in [0, {cap}) per sequence")
-        a64 = self.h64.numpy()
-        a32 = self.h32.numpy()
-        tables = a32[: cap * mb].reshape(cap, mb)
-        # Block-table rows: a host mirror per live sequence, refreshed only when its table grew.
-        live = {}
-        for i, s in enumerate(seqs):
-            p = s.num_cached_tokens
-            if s.num_tokens - p != pending:
-                raise ValueError("graph decode steps feed exactly one token per sequence")
-            row, known = self._rows.get(s.seq_id, (None, -1))
-            tbl = s.block_table
-            if row is None or known != len(tbl) or row[0] != tbl[0]:
-                row = np.zeros(mb, dtype=np.int32)
-                k = min(len(tbl), mb)
-                row[:k] = tbl[:k]
-                known = len(tbl)
-            live[s.seq_id] = (row, known)
-            tables[i] = row
-        self._rows = live
-        pos = np.fromiter((s.num_cached_tokens for s in seqs), dtype=np.int64, count=n)
-        covered = np.fromiter((v[1] for v in live.values()), dtype=np.int64, count=n) * bs
-        if n and (pos >= np.minimum(covered, self.max_ctx)).any():
-            raise ValueError("a sequence's block table does not cover the position it feeds")
-        if src_rows is None:
-            # The token at position num_cached_tokens is the sequence's last one.
-            a64[:n] = np.fromiter(((s.output_token_ids or s.prompt_token_ids)[-1] for s in seqs), np.int64, n)
-            a64[2 * cap : 2 * cap + n] = -1
-        else:
-            a64[:n] = 0
-            a64[2 * cap : 2 * cap + n] = src_rows
-        a64[2 * cap + n : 2 * cap + bucket] = -1
-        a64[cap : cap + n] = pos
-        # The decode kernel writes each row's new K/V into the slot of position pos (context pos + 1).
-        a32[cap * mb : cap * mb + n] = pos + 1
-        a64[n:bucket] = 0
-        a64[cap + n : cap + bucket] = 0
-        tables[n:bucket] = 0
-        a32[cap * mb + n : cap * mb + bucket] = 0  # padded rows write and attend to nothing
-        ctx = a32[cap * mb : cap * mb + bucket]
-        a32[cap * mb + cap : cap * mb + cap + bucket] = np.argsort(-ctx, kind="stable")  # longest first
+        if not isinstance(seqs, list):
+            seqs = list(seqs)
+        if src_rows is not None and not isinstance(src_rows, list):
+            src_rows = list(src_rows)
+        # Native: ids, positions, source rows, padded block tables, context lengths and the
+        # longest-first dispatch order, with the padding rows (context 0) up to the bucket.
+        _lib.native().fill_decode(seqs, bucket, src_rows, self.h64.data_ptr(), self.h64.numel(), self.h32.data_ptr(),
+                                  self.h32.numel(), self.capacity, self.max_blocks, self.block_size, self.max_ctx)
         self.d64.copy_(self.h64, non_blocking=True)
         self.d32.copy_(self.h32, non_blocking=True)
         self.copied.record()

@@ -23,7 +23,6 @@ from __future__ import annotations
 import math
 from typing import TYPE_CHECKING
 
-import numpy as np
 import torch
 
 from tokquay_amd import _lib
@@ -199,100 +198,107 @@ class PagedBatch(BatchedKV):
         error_word: torch.Tensor | None = None,
         partition_tokens: int = 0,
     ):
-        if not block_tables or not (len(block_tables) == len(start) == len(new_lens)):
-            raise ValueError("block_tables, start and new_lens must be non-empty and the same length")
-        if min(new_lens) < 1:
-            raise ValueError("every sequence must feed at least one token")
-        if min(start) < 0:
-            raise ValueError("start positions must be non-negative")
+        # Validation (the reference's conditions and messages, tokquay/kv_cache.py:182-191) and the packed
+        # metadata below are built by the native extension straight from the Python lists.
+        nat = _lib.native()
+        tables, start, new_lens = block_tables, start, new_lens
+        try:
+            plan = nat.plan(tables, start, new_lens, block_size)
+        except TypeError:  # the builder reads lists of ints; convert other sequences once
+            tables, start, new_lens = [list(t) for t in block_tables], list(start), list(new_lens)
+            plan = nat.plan(tables, start, new_lens, block_size)
         bs = block_size
-        ctx = [s + n for s, n in zip(start, new_lens)]  # keys visible after this step (tokquay/kv_cache.py:188)
-        for b, (tbl, c) in enumerate(zip(block_tables, ctx)):
-            if len(tbl) < cdiv(c, bs):
-                raise ValueError(f"sequence {b}: {len(tbl)} blocks cannot hold {c} tokens")
-
-        B, T = len(block_tables), max(new_lens)
+        B, T, N = len(tables), plan["T"], plan["N"]
+        Bd, Bp, nbd, nbp = plan["Bd"], plan["Bp"], plan["nbd"], plan["nbp"]
         self.pool, self.block_size, self.B, self.T = pool, bs, B, T
-        self.num_blocks_gathered = max(cdiv(c, bs) for c in ctx)
-        self.max_ctx = max(ctx)
-        self.start, self.new_lens, self.context_lens = list(start), list(new_lens), ctx
+        self.num_blocks_gathered = plan["max_blocks"]
+        self.max_ctx = plan["max_ctx"]
+        self.start, self.new_lens = start, new_lens
         self.error_word = error_word
         self.partition_tokens = partition_tokens
         device = pool.device
         self.device = device
-
-        dec = [b for b, n in enumerate(new_lens) if n == 1]
-        pre = [b for b, n in enumerate(new_lens) if n > 1]
-        Bd, Bp = len(dec), len(pre)
-        N = sum(new_lens)
         self.num_decode, self.num_prefill, self.num_tokens = Bd, Bp, N
-        nbd = max((cdiv(ctx[b], bs) for b in dec), default=0)
-        nbp = max((cdiv(ctx[b], bs) for b in pre), default=0)
-        self.decode_max_ctx = max((ctx[b] for b in dec), default=0)
-        self.prefill_max_q = max((new_lens[b] for b in pre), default=0)
+        self.decode_max_ctx = plan["decode_max_ctx"]
+        self.prefill_max_q = plan["prefill_max_q"]
         self._nbd, self._nbp = nbd, nbp
 
         pin = device.type == "cuda"
-        # int64 metadata: token_index[N] | positions[N] | slot_mapping[N] | last_rows[B]
-        h64 = torch.empty(3 * N + B, dtype=torch.int64, pin_memory=pin)
-        a64 = h64.numpy()
-        tok_idx, pos, slots, last = a64[:N], a64[N : 2 * N], a64[2 * N : 3 * N], a64[3 * N :]
-        # int32 metadata: dec_tables[Bd, nbd] | dec_ctx[Bd] | pre_tables[Bp, nbp] | pre_cu[Bp + 1] | pre_start[Bp]
-        # | dec_order[Bd] (decode rows, longest context first: the decode kernel's dispatch order)
-        n32 = Bd * nbd + Bd + Bp * nbp + (Bp + 1) + Bp + Bd
-        h32 = torch.zeros(n32, dtype=torch.int32, pin_memory=pin)
-        a32 = h32.numpy()
-        o_dt, o_dc = 0, Bd * nbd
-        o_pt = o_dc + Bd
-        o_pc = o_pt + Bp * nbp
-        o_ps = o_pc + Bp + 1
-        o_do = o_ps + Bp
-        dec_tables = a32[o_dt:o_dc].reshape(Bd, nbd)
-        pre_tables = a32[o_pt:o_pc].reshape(Bp, nbp)
-
-        for i, b in enumerate(dec):
-            tbl, p = block_tables[b], start[b]
-            tok_idx[i] = b * T
-            pos[i] = p
-            slots[i] = tbl[p // bs] * bs + p % bs
-            last[b] = i
-            k = cdiv(ctx[b], bs)
-            dec_tables[i, :k] = tbl[:k]  # the rest stays block 0 (padding, never read)
-            a32[o_dc + i] = ctx[b]
-        row = Bd
-        for i, b in enumerate(pre):
-            n, s = new_lens[b], start[b]
-            k = cdiv(ctx[b], bs)
-            tbl = np.asarray(block_tables[b][:k], dtype=np.int64)
-            ps = np.arange(s, s + n, dtype=np.int64)
-            tok_idx[row : row + n] = b * T + np.arange(n)
-            pos[row : row + n] = ps
-            slots[row : row + n] = tbl[ps // bs] * bs + ps % bs
-            last[b] = row + n - 1
-            pre_tables[i, :k] = tbl
-            a32[o_pc + i] = row - Bd
-            a32[o_ps + i] = s
-            row += n
-        a32[o_pc + Bp] = N - Bd
-        a32[o_do:] = np.argsort(-a32[o_dc:o_pt], kind="stable")
-
-        d64 = h64.to(device, non_blocking=True)
-        d32 = h32.to(device, non_blocking=True)
-        self.token_index = d64[:N]
-        self.packed_positions = d64[N : 2 * N]
-        self.slot_mapping = d64[2 * N : 3 * N]
-        self.last_rows = d64[3 * N :]
-        self.decode_block_tables = d32[o_dt:o_dc].view(Bd, nbd)
-        self.decode_context_lens = d32[o_dc:o_pt]
-        self.prefill_block_tables = d32[o_pt:o_pc].view(Bp, nbp)
-        self.prefill_cu_seqlens = d32[o_pc:o_ps]
-        self.prefill_start = d32[o_ps:o_do]
-        self.decode_order = d32[o_do:]
+        # int64: token_index[N] | positions[N] | slot_mapping[N] | last_rows[B]
+        # int32: dec_tables[Bd, nbd] | dec_ctx[Bd] | pre_tables[Bp, nbp] | pre_cu[Bp + 1] | pre_start[Bp]
+        #        | dec_order[Bd] (decode rows, longest context first: the decode kernel's dispatch order)
+        h64 = torch.empty(plan["n64"], dtype=torch.int64, pin_memory=pin)
+        h32 = torch.empty(plan["n32"], dtype=torch.int32, pin_memory=pin)
+        nat.fill(tables, start, new_lens, bs, h64.data_ptr(), h64.numel(), h32.data_ptr(), h32.numel())
+        self._d64 = h64.to(device, non_blocking=True)
+        self._d32 = h32.to(device, non_blocking=True)
+        # Element offsets of the int32 sections; the views below are made on first use.
+        self._o32 = (0, Bd * nbd, Bd * nbd + Bd, Bd * nbd + Bd + Bp * nbp, Bd * nbd + Bd + Bp * nbp + Bp + 1,
+                     Bd * nbd + Bd + Bp * nbp + 2 * Bp + 1)  # fmt: skip
         self._workspace: torch.Tensor | None = None
         self._ws_bytes = 0
         self._lazy: dict[str, torch.Tensor] = {}
 
+    # ---- device metadata views (sections of the two packed buffers) ----
+    def _view(self, name: str, buf: torch.Tensor, lo: int, hi: int, rows: int = -1) -> torch.Tensor:
+        t = self._lazy.get(name)
+        if t is None:
+            t = buf[lo:hi] if rows < 0 else buf[lo:hi].view(rows, -1 if rows else 0)
+            self._lazy[name] = t
+        return t
+
+    def _ptr32(self, i: int) -> int:
+        """Device address of int32 section ``i`` (dec_tables, dec_ctx, pre_tables, pre_cu, pre_start, dec_order)."""
+        return self._d32.data_ptr() + 4 * self._o32[i]
+
+    @property
+    def token_index(self) -> torch.Tensor:
+        """``[N]`` flat index ``b * T + t`` of each packed row's token."""
+        return self._view("token_index", self._d64, 0, self.num_tokens)
+
+    @property
+    def packed_positions(self) -> torch.Tensor:
+        return self._view("packed_positions", self._d64, self.num_tokens, 2 * self.num_tokens)
+
+    @property
+    def slot_mapping(self) -> torch.Tensor:
+        """``[N]`` pool slot (``block * block_size + offset``) of each packed row."""
+        return self._view("slot_mapping", self._d64, 2 * self.num_tokens, 3 * self.num_tokens)
+
+    @property
+    def last_rows(self) -> torch.Tensor:
+        return self._view("last_rows", self._d64, 3 * self.num_tokens, 3 * self.num_tokens + self.B)
+
+    @property
+    def decode_block_tables(self) -> torch.Tensor:
+        return self._view("decode_block_tables", self._d32, self._o32[0], self._o32[1], self.num_decode)
+
+    @property
+    def decode_context_lens(self) -> torch.Tensor:
+        return self._view("decode_context_lens", self._d32, self._o32[1], self._o32[2])
+
+    @property
+    def prefill_block_tables(self) -> torch.Tensor:
+        return self._view("prefill_block_tables", self._d32, self._o32[2], self._o32[3], self.num_prefill)
+
+    @property
+    def prefill_cu_seqlens(self) -> torch.Tensor:
+        return self._view("prefill_cu_seqlens", self._d32, self._o32[3], self._o32[4])
+
+    @property
+    def prefill_start(self) -> torch.Tensor:
+        return self._view("prefill_start", self._d32, self._o32[4], self._o32[5])
+
+    @property
+    def decode_order(self) -> torch.Tensor:
+        return self._view("decode_order", self._d32, self._o32[5], self._o32[5] + self.num_decode)
+
     # ---- reference contract members (built on demand; the HIP path does not need them) ----
+    @property
+    def context_lens(self) -> list[int]:
+        """Keys visible to each sequence after this step: ``start + new_len`` (tokquay/kv_cache.py:188)."""
+        return [s + n for s, n in zip(self.start, self.new_lens)]
+
     @property
     def positions(self) -> torch.Tensor:
         """``[B, T]`` absolute position of every (padded) new token (tokquay/kv_cache.py:205)."""
@@ -347,7 +353,9 @@ class PagedBatch(BatchedKV):
         Launches, all on the current stream: decode attention for the one-token rows
         with their cache write folded in (``tq_paged_decode_write``), then - for the
         rows of sequences feeding several tokens - their cache write and prefill
-        attention.
+        attention. One call into the native extension makes all of them; with a
+        ``launch_hook`` set they go one by one through ctypes, the hook before each
+        attention kernel.
         """
         pool = self.pool
         nb, n_layer, _, n_head, bs, d = pool.shape
@@ -366,37 +374,46 @@ class PagedBatch(BatchedKV):
         row3 = 3 * C
         qp, pp, op = qkv.data_ptr(), pool.data_ptr(), out.data_ptr()
         scale = 1.0 / math.sqrt(d)
+        Bd, Bp = self.num_decode, self.num_prefill
+        if Bd and self._workspace is None:
+            self._ws_bytes = int(L.tq_paged_decode_workspace_size(Bd, n_head, d, self.decode_max_ctx, self.partition_tokens))
+            self._workspace = torch.empty(max(self._ws_bytes, 1), dtype=torch.uint8, device=pool.device)
+        ws = self._workspace.data_ptr() if Bd else 0
+        slots = self._d64.data_ptr() + 8 * 2 * N
 
-        Bd = self.num_decode
+        if PagedBatch.launch_hook is None:  # one native call launches the whole layer
+            failed = _lib.native().attend(
+                op, qp, pp, nb, n_layer, n_head, bs, d, layer, scale, stream, err or 0, N,
+                Bd, self._ptr32(0), self._nbd, self._ptr32(1), self._ptr32(5), self.decode_max_ctx,
+                self.partition_tokens, ws, self._ws_bytes,
+                Bp, slots, self._ptr32(2), self._nbp, self._ptr32(3), self._ptr32(4), self.prefill_max_q,
+            )  # fmt: skip
+            if failed is not None:
+                _lib.check(*failed)
+            return out
+
+        # Per-kernel launches, with the hook armed before each attention kernel.
         if Bd:
-            if self._workspace is None:
-                self._ws_bytes = int(L.tq_paged_decode_workspace_size(Bd, n_head, d, self.decode_max_ctx, self.partition_tokens))
-                self._workspace = torch.empty(max(self._ws_bytes, 1), dtype=torch.uint8, device=pool.device)
-            if PagedBatch.launch_hook is not None:
-                PagedBatch.launch_hook(self, "decode")
+            PagedBatch.launch_hook(self, "decode")
             _lib.check(
                 L.tq_paged_decode_write(op, C, qp, row3, qp + 4 * C, row3, qp + 8 * C, row3, pp, nb, n_layer,
-                                        n_head, bs, d, layer, self.decode_block_tables.data_ptr(), self._nbd,
-                                        self._nbd, self.decode_context_lens.data_ptr(), self.decode_order.data_ptr(),
-                                        Bd, self.decode_max_ctx,
-                                        scale, self.partition_tokens, self._workspace.data_ptr(), self._ws_bytes,
-                                        err, stream),
+                                        n_head, bs, d, layer, self._ptr32(0), self._nbd, self._nbd, self._ptr32(1),
+                                        self._ptr32(5), Bd, self.decode_max_ctx, scale, self.partition_tokens, ws,
+                                        self._ws_bytes, err, stream),
                 "tq_paged_decode_write",
             )  # fmt: skip
-        if self.num_prefill:
+        if Bp:
             off = Bd * row3 * 4  # bytes to the first prefill row of qkv
             _lib.check(
                 L.tq_cache_write(pp, nb, n_layer, n_head, bs, d, layer, qp + off + 4 * C, row3, qp + off + 8 * C,
-                                 row3, self.slot_mapping.data_ptr() + 8 * Bd, N - Bd, err, stream),
+                                 row3, slots + 8 * Bd, N - Bd, err, stream),
                 "tq_cache_write",
             )  # fmt: skip
-            if PagedBatch.launch_hook is not None:
-                PagedBatch.launch_hook(self, "prefill")
+            PagedBatch.launch_hook(self, "prefill")
             _lib.check(
-                L.tq_paged_prefill(op + 4 * Bd * C, C, qp + 4 * Bd * row3, row3, pp, nb, n_layer, n_head, bs, d, layer,
-                                   self.prefill_block_tables.data_ptr(), self._nbp, self._nbp,
-                                   self.prefill_cu_seqlens.data_ptr(), self.prefill_start.data_ptr(),
-                                   self.num_prefill, N - Bd, self.prefill_max_q, scale, err, stream),
+                L.tq_paged_prefill(op + 4 * Bd * C, C, qp + off, row3, pp, nb, n_layer, n_head, bs, d, layer,
+                                   self._ptr32(2), self._nbp, self._nbp, self._ptr32(3), self._ptr32(4), Bp, N - Bd,
+                                   self.prefill_max_q, scale, err, stream),
                 "tq_paged_prefill",
             )  # fmt: skip
         return out
