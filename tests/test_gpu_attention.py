@@ -64,6 +64,15 @@ def test_decode_edge_contexts(block_size, partition_tokens):
     check(sc, partition_tokens)
 
 
+@pytest.mark.parametrize("partition_tokens", [16, 32])
+def test_decode_more_than_64_partitions(partition_tokens):
+    """Contexts past 1024 positions at short partitions: up to 188 partitions per sequence, which
+    the merge takes 64 at a time (65 = one full pass and one partition)."""
+    ctx = [1040, 1025, 3000, 65 * 16, 64 * 16, 17]
+    sc = Scenario([c - 1 for c in ctx], [1] * len(ctx), block_size=16, seed=21)
+    check(sc, partition_tokens)
+
+
 @pytest.mark.parametrize("block_size", [1, 16, 32])
 @pytest.mark.parametrize("partition_tokens", [0, 16, 1024])
 def test_decode_write_equals_cache_write_then_decode(block_size, partition_tokens):

@@ -368,7 +368,24 @@ __global__ __launch_bounds__(kWave* kHeadsPerGroup) void decode_partition_kernel
   }
 }
 
-// Log-sum-exp merge of a sequence's partitions: one wave per (sequence, head), lane = dim.
+// Log-sum-exp merge of a sequence's partitions: one wave per (sequence, head). Up to 64
+// partitions at a time, lane p holds partition p's (m, l): the max and the weights
+// exp(m_p - M) come from cross-lane reductions, so the loads of one pass are all
+// independent; then lane = dim accumulates the weighted partial outputs, eight
+// partitions per unrolled step (rows past the last partition are clamped to it
+// and weighted 0).
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum_f(float v) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
 __global__ __launch_bounds__(kWave* kHeadsPerGroup) void decode_merge_kernel(const DecodeArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
   const int h = blockIdx.x * kHeadsPerGroup + (threadIdx.x / kWave);
@@ -379,13 +396,29 @@ __global__ __launch_bounds__(kWave* kHeadsPerGroup) void decode_merge_kernel(con
   if (nparts <= 1) return;  // written directly by the partition kernel
   const float* pp = a.partials + ((int64_t)b * a.num_heads + h) * a.max_parts * kPartialStride;
   float M = -INFINITY;
-  for (int p = 0; p < nparts; ++p) M = fmaxf(M, pp[p * kPartialStride + kHeadDim]);
+  for (int p0 = 0; p0 < nparts; p0 += kWave) {
+    const int p = p0 + lane;
+    M = fmaxf(M, wave_max_f(p < nparts ? pp[p * kPartialStride + kHeadDim] : -INFINITY));
+  }
   float L = 0.f, O = 0.f;
-  for (int p = 0; p < nparts; ++p) {
-    const float mp = pp[p * kPartialStride + kHeadDim];
-    const float w = mp == -INFINITY ? 0.f : __expf(mp - M);
-    L = fmaf(pp[p * kPartialStride + kHeadDim + 1], w, L);
-    O = fmaf(pp[p * kPartialStride + lane], w, O);
+  for (int p0 = 0; p0 < nparts; p0 += kWave) {
+    const int p = p0 + lane;
+    float w = 0.f, lw = 0.f;
+    if (p < nparts) {
+      const float mp = pp[p * kPartialStride + kHeadDim];
+      w = mp == -INFINITY ? 0.f : __expf(mp - M);
+      lw = pp[p * kPartialStride + kHeadDim + 1] * w;
+    }
+    L += wave_sum_f(lw);
+    const int cnt = min(kWave, nparts - p0);
+    for (int j0 = 0; j0 < cnt; j0 += 8) {  // j0 + 7 < 64: cnt rounded up to 8 is at most 64
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int row = min(p0 + j0 + u, nparts - 1);
+        const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j0 + u));
+        O = fmaf(pp[row * kPartialStride + lane], wj, O);
+      }
+    }
   }
   a.out[(int64_t)b * a.out_stride + h * kHeadDim + lane] = O / L;
 }
