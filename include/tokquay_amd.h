@@ -13,6 +13,9 @@
  *
  *   tq_argmax_rows    index of each logit row's maximum (greedy sampling)
  *   tq_add_layernorm  residual add fused with the LayerNorm that follows it
+ *   tq_skinny_linear  linear layer of at most 16 rows, LayerNorm / bias / GELU /
+ *                     residual add fused in (small-batch decode steps)
+ *   tq_embed_rows     token + position embeddings of each row
  *
  * KV pool layout (identical to the reference's, bit for bit):
  *
@@ -233,6 +236,42 @@ tq_status tq_add_layernorm(float* x_out, int64_t x_out_stride, float* h_out, int
                            const float* x, int64_t x_stride, const float* y, int64_t y_stride,
                            const float* gamma, const float* beta, int64_t rows, int32_t cols,
                            float eps, void* stream);
+
+/*
+ * Linear layer of a few rows with its neighbours fused in:
+ *
+ *   h = LN(x) if ln_gamma else x        (LN over K, biased variance, eps = ln_eps)
+ *   v = h W^T + bias                    (bias may be NULL)
+ *   epilogue 0: y = v;  1: y = gelu_tanh(v);  2: y = y + v (residual add, in place)
+ *
+ * x [M, K] (row stride x_stride), W [N, K] contiguous (nn.Linear's [out, in]),
+ * y [M, N] (row stride y_stride), all fp32. M <= 16; K = 768, or K = 3072 without
+ * the LayerNorm (GPT-2's widths; other shapes return TQ_ERR_UNSUPPORTED); x, W,
+ * ln_gamma, ln_beta 16-byte aligned, x_stride a multiple of 4. y must not overlap
+ * x. Reads W once; the partial products of the K slices are summed in a fixed
+ * order (repeated calls give the same bits).
+ *
+ * Replaces, for decode steps of at most 16 sequences, the c_attn / c_proj / c_fc
+ * / mlp.c_proj linears (tokquay/model.py:62-63, :103-104) with ln_1 / ln_2 in
+ * front (:117-118), the GELU (:107) and the residual adds (:122-123), and the
+ * LM head with ln_f (:180-181, W = wte, no bias).
+ */
+tq_status tq_skinny_linear(float* y, int64_t y_stride, const float* x, int64_t x_stride, int32_t M,
+                           const float* w, const float* bias, int32_t N, int32_t K, const float* ln_gamma,
+                           const float* ln_beta, float ln_eps, int32_t epilogue, void* stream);
+
+/*
+ * x[r] = wte[id_r] + wpe[positions[r]] for rows r < rows, C columns (a multiple
+ * of 4), x row stride x_stride. id_r = tokens[src[r]] when src is not NULL and
+ * src[r] >= 0 (the token a previous step chose for row src[r], left on the
+ * device), else ids[r]. Ids outside [0, vocab) or positions outside
+ * [0, n_positions) set TQ_DEVERR_LENGTH in d_error and are clamped.
+ * Replaces the embedding sum of GPT2.forward (tokquay/model.py:172).
+ */
+tq_status tq_embed_rows(float* x, int64_t x_stride, const int64_t* ids, const int64_t* src,
+                        const int64_t* tokens, const int64_t* positions, const float* wte, const float* wpe,
+                        int64_t rows, int32_t C, int64_t vocab, int64_t n_positions, int32_t* d_error,
+                        void* stream);
 
 #ifdef __cplusplus
 }

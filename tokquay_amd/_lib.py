@@ -95,6 +95,22 @@ SIGNATURES: dict[str, tuple] = {
             c_f32p, c_f32p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float, ctypes.c_void_p,  # gamma, beta, rows, cols, eps, stream
         ],
     ),
+    "tq_skinny_linear": (
+        ctypes.c_int,
+        [
+            c_f32p, ctypes.c_int64, c_f32p, ctypes.c_int64, ctypes.c_int32,  # y, y_stride, x, x_stride, M
+            c_f32p, c_f32p, ctypes.c_int32, ctypes.c_int32,  # w, bias, N, K
+            c_f32p, c_f32p, ctypes.c_float, ctypes.c_int32, ctypes.c_void_p,  # ln_gamma, ln_beta, ln_eps, epilogue, stream
+        ],
+    ),
+    "tq_embed_rows": (
+        ctypes.c_int,
+        [
+            c_f32p, ctypes.c_int64, c_i64p, c_i64p, c_i64p, c_i64p,  # x, x_stride, ids, src, tokens, positions
+            c_f32p, c_f32p, ctypes.c_int64, ctypes.c_int32,  # wte, wpe, rows, C
+            ctypes.c_int64, ctypes.c_int64, c_i32p, ctypes.c_void_p,  # vocab, n_positions, d_error, stream
+        ],
+    ),
     "tq_argmax_rows": (
         ctypes.c_int,
         [c_i64p, c_f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p],  # out, logits, rows, cols, row_stride, stream

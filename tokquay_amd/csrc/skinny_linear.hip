@@ -1,0 +1,333 @@
+// Linear layers of small decode batches (at most 16 rows), with the LayerNorm in
+// front of them and the bias / GELU / residual add after them fused in:
+//
+//   y = epilogue( LN(x) W^T + b )      x [M, K], W [N, K] (nn.Linear layout), M <= 16
+//
+// At a few rows a linear layer is a weight stream: every weight is used M times,
+// so the launch is bound by reading W from HBM once, and by latency. The library
+// GEMMs take ~9-10 us per call at these shapes; a decode step at batch 1-16 has 4
+// of them per layer plus the LayerNorm, GELU and residual-add launches between
+// them. This kernel makes each linear layer one launch that reads W once.
+//
+// Y^T[n][m] = sum_k W[n][k] X[m][k] on v_mfma_f32_16x16x4_f32: the A operand is 16
+// rows of W, the B operand X^T, so one MFMA block covers the whole batch (rows past M
+// are zero). Lane (i, g) = (lane % 16, lane / 16) loads W[n0 + i][k .. k + 3] and
+// X[i][k .. k + 3] with k = kb + 4 g as float4s; step j = 0..3 of the block then
+// takes component j, so lane group g supplies k = kb + 4 g + j to both operands.
+// The accumulator's lane (j, g) holds Y^T[n0 + 4 g + r][m = j], r = 0..3.
+//
+// Work split: a wave owns one 192-wide k slice (each lane keeps its part of X in 12
+// float4 registers) of 16 R output columns; a workgroup's KW = K / 192 waves cover
+// all of K, and their partial products are summed through LDS in a fixed order.
+// Every load of W is issued before anything waits: block r + 1 while block r is
+// multiplied. (The 768-column layers leave most CUs idle - 48 column blocks - but
+// splitting their K over workgroups costs more than it saves: a cross-XCD
+// reduction needs an L2 write-back per workgroup, and deferring the sum to the
+// next launch makes every one of its workgroups read all the partial products.)
+//
+// The LayerNorm (whole K in one workgroup) normalises X in registers: two-pass row
+// statistics over the registers, combined across the waves through LDS, with gamma
+// and beta staged in LDS. The residual epilogue adds into y in place
+// (y = y + (x W^T + b)), the reference's x = x + sublayer(...) at
+// tokquay/model.py:122-123; GELU is the tanh form of tokquay/model.py:107.
+//
+// Reference semantics: nn.Linear (tokquay/model.py:62-63, :103-104), LayerNorm
+// (:117-118, :145), tied LM head (:180).
+
+#include "tq_internal.h"
+
+namespace tq {
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kSkinnyRows = 16;
+constexpr int kSkinnyT = 12;                  // float4 steps of 16 k per wave
+constexpr int kSkinnyRange = 16 * kSkinnyT;  // k per wave (one slice)
+
+enum Epilogue { kEpiBias = 0, kEpiGelu = 1, kEpiResidual = 2 };
+
+struct SkinnyArgs {
+  float* y;
+  int64_t y_stride;
+  const float* x;
+  int64_t x_stride;
+  const float* w;
+  const float* bias;   // may be null
+  const float* gamma;  // LayerNorm weight / bias (fused LN only)
+  const float* beta;
+  float eps;
+  int32_t M;
+  int32_t N;
+  int32_t K;
+};
+
+__device__ __forceinline__ float gelu_tanh(float v) {
+  const float kBeta = 0.7978845608028654f;  // sqrt(2 / pi)
+  const float kKappa = 0.044715f;
+  return 0.5f * v * (1.f + tanhf(kBeta * (v + kKappa * v * v * v)));
+}
+
+template <int EPI>
+__device__ __forceinline__ void store_output(const SkinnyArgs& a, int m, int n, float v) {
+  if (a.bias != nullptr) v += a.bias[n];
+  float* yp = a.y + (int64_t)m * a.y_stride + n;
+  if constexpr (EPI == kEpiGelu) v = gelu_tanh(v);
+  if constexpr (EPI == kEpiResidual) v = *yp + v;
+  *yp = v;
+}
+
+template <int KW, int R, bool LN, int EPI>
+__global__ __launch_bounds__(kWave* KW) void skinny_linear_kernel(const SkinnyArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int i = lane & 15;
+  const int g = lane >> 4;
+  const int k_lo = wave * kSkinnyRange;
+  const int n_base = blockIdx.x * (16 * R);
+
+  // gamma / beta first (needed first, after the X loads), staged to LDS for the whole K.
+  // K / 4 = 48 KW float4s of each: at most one per thread.
+  constexpr int kLnVec = KW * kSkinnyRange / 4;
+  __shared__ float4 s_gamma[LN ? kLnVec : 1], s_beta[LN ? kLnVec : 1];
+  float4 gm_ld = make_float4(0.f, 0.f, 0.f, 0.f), bt_ld = gm_ld;
+  if constexpr (LN) {
+    const int j = min((int)threadIdx.x, kLnVec - 1);
+    gm_ld = reinterpret_cast<const float4*>(a.gamma)[j];
+    bt_ld = reinterpret_cast<const float4*>(a.beta)[j];
+  }
+
+  // This lane's slice of X: row i, k = k_lo + 16 t + 4 g + 0..3.
+  float4 xr[kSkinnyT];
+  if (i < a.M) {
+    const float* xp = a.x + (int64_t)i * a.x_stride + k_lo + 4 * g;
+#pragma unroll
+    for (int t = 0; t < kSkinnyT; ++t) xr[t] = *reinterpret_cast<const float4*>(xp + 16 * t);
+  } else {  // rows past the batch are zero
+#pragma unroll
+    for (int t = 0; t < kSkinnyT; ++t) xr[t] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+
+  // W rows n_base + 16 r + i; rows past N (the ragged last block) read row N - 1 and are not
+  // stored. Block 0 is issued before anything waits; block r + 1 while block r is multiplied.
+  auto load_w = [&](floatx4 (&wv)[kSkinnyT], int r) {
+    const int n = min(n_base + 16 * r + i, a.N - 1);
+    const float* wp = a.w + (int64_t)n * a.K + k_lo + 4 * g;
+#pragma unroll
+    for (int t = 0; t < kSkinnyT; ++t)
+      wv[t] = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(wp + 16 * t));
+  };
+  floatx4 wb[R > 1 ? 2 : 1][kSkinnyT];
+  load_w(wb[0], 0);
+  __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of everything below
+
+  if constexpr (LN) {
+    if ((int)threadIdx.x < kLnVec) {
+      s_gamma[threadIdx.x] = gm_ld;
+      s_beta[threadIdx.x] = bt_ld;
+    }
+    // Row i's sum over this wave's slice lives in lanes i, i + 16, i + 32, i + 48.
+    __shared__ float red[2][KW][kSkinnyRows];
+    float sum = 0.f;
+#pragma unroll
+    for (int t = 0; t < kSkinnyT; ++t) sum += (xr[t].x + xr[t].y) + (xr[t].z + xr[t].w);
+    sum += __shfl_xor(sum, 16);
+    sum += __shfl_xor(sum, 32);
+    if (g == 0) red[0][wave][i] = sum;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < KW; ++w) tot += red[0][w][i];
+    const float inv_k = 1.f / (float)a.K;
+    const float mean = tot * inv_k;
+    float q = 0.f;
+#pragma unroll
+    for (int t = 0; t < kSkinnyT; ++t) {
+      const float dx = xr[t].x - mean, dy = xr[t].y - mean, dz = xr[t].z - mean, dw = xr[t].w - mean;
+      q += (dx * dx + dy * dy) + (dz * dz + dw * dw);
+    }
+    q += __shfl_xor(q, 16);
+    q += __shfl_xor(q, 32);
+    if (g == 0) red[1][wave][i] = q;
+    __syncthreads();
+    tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < KW; ++w) tot += red[1][w][i];
+    const float rstd = rsqrtf(tot * inv_k + a.eps);
+#pragma unroll
+    for (int t = 0; t < kSkinnyT; ++t) {
+      const int j = (k_lo + 16 * t + 4 * g) / 4;
+      const float4 gm = s_gamma[j];
+      const float4 bt = s_beta[j];
+      xr[t].x = (xr[t].x - mean) * rstd * gm.x + bt.x;
+      xr[t].y = (xr[t].y - mean) * rstd * gm.y + bt.y;
+      xr[t].z = (xr[t].z - mean) * rstd * gm.z + bt.z;
+      xr[t].w = (xr[t].w - mean) * rstd * gm.w + bt.w;
+    }
+  }
+
+  floatx4 acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (r + 1 < R) {
+      load_w(wb[(r + 1) & 1], r + 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const floatx4(&wv)[kSkinnyT] = wb[r & 1];
+    acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < kSkinnyT; ++t) {
+      acc[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][0], xr[t].x, acc[r], 0, 0, 0);
+      acc[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][1], xr[t].y, acc[r], 0, 0, 0);
+      acc[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][2], xr[t].z, acc[r], 0, 0, 0);
+      acc[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][3], xr[t].w, acc[r], 0, 0, 0);
+    }
+  }
+
+  // Partial products of the KW waves: part[w][r][lane][reg], 5 floats per lane (bank spread).
+  __shared__ float part[KW][R][kWave][5];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) part[wave][r][lane][q] = acc[r][q];
+  __syncthreads();
+
+  // Output o = (m, nn): m = o / (16 R), column n_base + nn. Its value sits in lane m + 16 (c / 4),
+  // register c % 4 of block nn / 16, c = nn % 16.
+  for (int o = threadIdx.x; o < 16 * kSkinnyRows * R; o += kWave * KW) {
+    const int m = o / (16 * R);
+    const int nn = o - m * (16 * R);
+    const int n = n_base + nn;
+    if (m >= a.M || n >= a.N) continue;
+    const int c = nn & 15;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < KW; ++w) v += part[w][nn >> 4][m + 16 * (c >> 2)][c & 3];
+    store_output<EPI>(a, m, n, v);
+  }
+}
+
+template <int KW, int R, bool LN>
+void launch_skinny_epi(const SkinnyArgs& a, int epi, hipStream_t s) {
+  const dim3 grid((unsigned)((a.N + 16 * R - 1) / (16 * R))), block(kWave * KW);
+  switch (epi) {
+    case kEpiGelu: hipLaunchKernelGGL((skinny_linear_kernel<KW, R, LN, kEpiGelu>), grid, block, 0, s, a); break;
+    case kEpiResidual:
+      hipLaunchKernelGGL((skinny_linear_kernel<KW, R, LN, kEpiResidual>), grid, block, 0, s, a);
+      break;
+    default: hipLaunchKernelGGL((skinny_linear_kernel<KW, R, LN, kEpiBias>), grid, block, 0, s, a); break;
+  }
+}
+
+// Waves per workgroup (K / 192) and column blocks per workgroup for (N, K, LN); {0, 0} when unsupported.
+struct SkinnyShape {
+  int kw, r;
+};
+
+SkinnyShape skinny_shape(int32_t N, int32_t K, bool ln) {
+  if (K % kSkinnyRange != 0) return {0, 0};
+  const int slices = K / kSkinnyRange;
+  if (slices == 4) return N > 8192 ? SkinnyShape{4, 4} : SkinnyShape{4, 1};  // wide: the LM head
+  if (slices == 16 && !ln) return {16, 1};  // 1024-thread workgroups: one column block fits the registers
+  return {0, 0};
+}
+
+// ------------------------------------------------------------------------------- embeddings
+// x[r] = wte[id_r] + wpe[pos_r]; id_r = tokens[src[r]] when src (optional) has src[r] >= 0,
+// else ids[r] (tokquay/model.py:172). One 64-lane wave per row, float4 columns. Ids or
+// positions out of range are reported (TQ_DEVERR_LENGTH) and clamped so every read
+// stays inside the tables.
+__global__ __launch_bounds__(256) void embed_rows_kernel(float* x, int64_t x_stride, const int64_t* ids,
+                                                         const int64_t* src, const int64_t* tokens,
+                                                         const int64_t* positions, const float* wte,
+                                                         const float* wpe, int64_t rows, int32_t C, int64_t vocab,
+                                                         int64_t n_pos, int32_t* d_error) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t r = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
+  if (r >= rows) return;
+  int64_t id = ids[r];
+  if (src != nullptr) {
+    const int64_t sr = src[r];
+    if (sr >= 0) id = tokens[sr];
+  }
+  int64_t pos = positions[r];
+  if (id < 0 || id >= vocab || pos < 0 || pos >= n_pos) {
+    if (lane == 0) flag_error(d_error, TQ_DEVERR_LENGTH);
+    id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);
+    pos = pos < 0 ? 0 : (pos >= n_pos ? n_pos - 1 : pos);
+  }
+  const float* te = wte + id * C;
+  const float* pe = wpe + pos * C;
+  float* xo = x + r * x_stride;
+  for (int c = 4 * lane; c < C; c += 4 * kWave) {
+    const float4 u = *reinterpret_cast<const float4*>(te + c);
+    const float4 v = *reinterpret_cast<const float4*>(pe + c);
+    *reinterpret_cast<float4*>(xo + c) = make_float4(u.x + v.x, u.y + v.y, u.z + v.z, u.w + v.w);
+  }
+}
+
+}  // namespace
+}  // namespace tq
+
+extern "C" tq_status tq_skinny_linear(float* y, int64_t y_stride, const float* x, int64_t x_stride, int32_t M,
+                                      const float* w, const float* bias, int32_t N, int32_t K,
+                                      const float* ln_gamma, const float* ln_beta, float ln_eps, int32_t epilogue,
+                                      void* stream) {
+  using namespace tq;
+  if (M < 0 || N < 1 || K < 1 || epilogue < 0 || epilogue > 2) return TQ_ERR_INVALID_ARGUMENT;
+  if ((ln_gamma == nullptr) != (ln_beta == nullptr) || (ln_gamma != nullptr && !(ln_eps >= 0.f)))
+    return TQ_ERR_INVALID_ARGUMENT;
+  if (M > kSkinnyRows) return TQ_ERR_UNSUPPORTED;
+  const bool ln = ln_gamma != nullptr;
+  const SkinnyShape sh = skinny_shape(N, K, ln);
+  if (sh.kw == 0) return TQ_ERR_UNSUPPORTED;
+  if (M == 0) return TQ_OK;
+  if (y == nullptr || x == nullptr || w == nullptr) return TQ_ERR_INVALID_ARGUMENT;
+  if (x_stride < K || y_stride < N) return TQ_ERR_INVALID_ARGUMENT;
+  if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)ln_gamma | (uintptr_t)ln_beta) % 16 != 0 || x_stride % 4 != 0)
+    return TQ_ERR_INVALID_ARGUMENT;
+  SkinnyArgs a;
+  a.y = y;
+  a.y_stride = y_stride;
+  a.x = x;
+  a.x_stride = x_stride;
+  a.w = w;
+  a.bias = bias;
+  a.gamma = ln_gamma;
+  a.beta = ln_beta;
+  a.eps = ln_eps;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  hipStream_t s = (hipStream_t)stream;
+  if (sh.r == 4) {  // wide outputs
+    if (ln) launch_skinny_epi<4, 4, true>(a, epilogue, s);
+    else launch_skinny_epi<4, 4, false>(a, epilogue, s);
+  } else if (sh.kw == 4) {
+    if (ln) launch_skinny_epi<4, 1, true>(a, epilogue, s);
+    else launch_skinny_epi<4, 1, false>(a, epilogue, s);
+  } else {
+    launch_skinny_epi<16, 1, false>(a, epilogue, s);
+  }
+  return check_launch();
+}
+
+extern "C" tq_status tq_embed_rows(float* x, int64_t x_stride, const int64_t* ids, const int64_t* src,
+                                   const int64_t* tokens, const int64_t* positions, const float* wte,
+                                   const float* wpe, int64_t rows, int32_t C, int64_t vocab, int64_t n_positions,
+                                   int32_t* d_error, void* stream) {
+  using namespace tq;
+  if (rows < 0 || C < 1 || vocab < 1 || n_positions < 1) return TQ_ERR_INVALID_ARGUMENT;
+  if (C % 4 != 0) return TQ_ERR_UNSUPPORTED;
+  if (rows == 0) return TQ_OK;
+  if (x == nullptr || ids == nullptr || positions == nullptr || wte == nullptr || wpe == nullptr ||
+      (src != nullptr && tokens == nullptr))
+    return TQ_ERR_INVALID_ARGUMENT;
+  if (x_stride < C || x_stride % 4 != 0 || ((uintptr_t)x | (uintptr_t)wte | (uintptr_t)wpe) % 16 != 0)
+    return TQ_ERR_INVALID_ARGUMENT;
+  const int64_t groups = (rows + 3) / 4;
+  if (groups > 0x7fffffffLL) return TQ_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(embed_rows_kernel, dim3((unsigned)groups), dim3(256), 0, (hipStream_t)stream, x, x_stride, ids,
+                     src, tokens, positions, wte, wpe, rows, C, vocab, n_positions, d_error);
+  return check_launch();
+}

@@ -128,8 +128,11 @@ class StaticDecodeView:
 class DecodeGraphs:
     """Captured decode forwards, one per batch bucket, sharing one StaticDecodeBatch."""
 
-    def __init__(self, model, allocator: BlockAllocator, max_batch: int):
+    def __init__(self, model, allocator: BlockAllocator, max_batch: int, skinny: bool = True):
+        """``skinny``: buckets of at most 16 rows run the fused small-batch linears
+        (``GPT2.skinny_logits``) instead of the library GEMMs."""
         self.model = model
+        self.skinny = skinny
         self.static = StaticDecodeBatch(allocator, bucket_for(max_batch), model.cfg.n_positions)
         self.graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
 
@@ -140,9 +143,16 @@ class DecodeGraphs:
     def _forward(self, rows: int) -> torch.Tensor:
         m, s = self.model, self.static
         view = s.view(rows)
-        src = s.src[:rows]
-        ids = torch.where(src >= 0, s.tokens.index_select(0, src.clamp(min=0)), s.ids[:rows])
-        logits = m.trunk(ids, s.positions[:rows], view) @ m.wte.weight.T
+        if self.skinny and m.skinny_ok(rows):
+            # Up to 16 rows: embeddings (source rows resolved on the device) and five launches per
+            # layer, each linear with its LayerNorm / GELU / residual add fused in.
+            x = ops.embed_rows(s.ids[:rows], s.positions[:rows], m.wte.weight, m.wpe.weight, src=s.src[:rows],
+                               tokens=s.tokens, error_word=s.error_word)  # fmt: skip
+            logits = m.skinny_logits(x, view)
+        else:
+            src = s.src[:rows]
+            ids = torch.where(src >= 0, s.tokens.index_select(0, src.clamp(min=0)), s.ids[:rows])
+            logits = m.trunk(ids, s.positions[:rows], view) @ m.wte.weight.T
         ops.argmax_rows(logits, out=s.tokens[:rows])
         return logits
 

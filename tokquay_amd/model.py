@@ -99,6 +99,29 @@ class GPT2(nn.Module):
             x, h = ops.add_layernorm(x, block.mlp(h), nxt.weight, nxt.bias, nxt.eps, x_out=x)
         return h
 
+    def skinny_ok(self, rows: int) -> bool:
+        """Whether a batch of ``rows`` can run through :meth:`skinny_logits` (at most 16 rows; the
+        linears' input widths n_embd and 4 * n_embd must be ones ``tq_skinny_linear`` takes)."""
+        C = self.cfg.n_embd
+        return ops.skinny_supported(rows, C) and ops.skinny_supported(rows, 4 * C)
+
+    def skinny_logits(self, x: torch.Tensor, cache) -> torch.Tensor:
+        """Logits ``[M, vocab]`` of ``M <= 16`` rows from their embeddings ``x`` ``[M, C]``, which become
+        the residual stream (updated in place). The reference's loop (tokquay/model.py:172-181) as five
+        launches per block: ``c_attn`` with ``ln_1`` in front, attention, ``c_proj`` adding into x,
+        ``c_fc`` with ``ln_2`` in front and the GELU after, ``mlp.c_proj`` adding into x; then the tied
+        LM head with ``ln_f`` in front (``tq_skinny_linear``)."""
+        for i, block in enumerate(self.h):
+            at, mlp = block.attn, block.mlp
+            qkv = ops.skinny_linear(x, at.c_attn.weight, at.c_attn.bias,
+                                    ln=(block.ln_1.weight, block.ln_1.bias, block.ln_1.eps))  # fmt: skip
+            a = cache.attend(i, qkv)
+            ops.skinny_linear(a, at.c_proj.weight, at.c_proj.bias, epilogue="residual", out=x)
+            h = ops.skinny_linear(x, mlp.c_fc.weight, mlp.c_fc.bias, ln=(block.ln_2.weight, block.ln_2.bias,
+                                                                        block.ln_2.eps), epilogue="gelu")  # fmt: skip
+            ops.skinny_linear(h, mlp.c_proj.weight, mlp.c_proj.bias, epilogue="residual", out=x)
+        return ops.skinny_linear(x, self.wte.weight, None, ln=(self.ln_f.weight, self.ln_f.bias, self.ln_f.eps))
+
     def forward(self, input_ids: torch.Tensor, cache: PagedBatch, last_only: bool = False) -> torch.Tensor:
         """input_ids ``[B, T]`` (new tokens, right-padded) -> logits ``[B, T, vocab]``, or ``[B, 1, vocab]``
         of each row's last real token when ``last_only``. Validation follows tokquay/model.py:154-160."""

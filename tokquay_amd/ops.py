@@ -242,3 +242,83 @@ def add_layernorm(x: torch.Tensor, y: torch.Tensor, weight: torch.Tensor, bias: 
                                      float(eps), _stream(x.device))  # fmt: skip
     _lib.check(st, "tq_add_layernorm")
     return x_out, h
+
+
+SKINNY_MAX_ROWS = 16
+SKINNY_WIDTHS = (768, 3072)
+_EPILOGUES = {"none": 0, "gelu": 1, "residual": 2}
+
+
+def skinny_supported(rows: int, in_features: int) -> bool:
+    """Whether ``tq_skinny_linear`` takes this shape (at most 16 rows, K = 768 or 3072)."""
+    return 0 < rows <= SKINNY_MAX_ROWS and in_features in SKINNY_WIDTHS
+
+
+def skinny_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
+                  ln: tuple[torch.Tensor, torch.Tensor, float] | None = None, epilogue: str = "none",
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """``epilogue(LN(x) @ weight.T + bias)`` for at most 16 float32 rows in one launch (``tq_skinny_linear``).
+
+    ``ln = (gamma, beta, eps)`` fuses the LayerNorm in front (tokquay/model.py:117-118); ``epilogue`` is
+    ``"none"``, ``"gelu"`` (tanh form, :107) or ``"residual"``: ``out += x @ weight.T + bias`` in place (the
+    residual add, :122-123; ``out`` required). ``weight`` is nn.Linear's ``[N, K]``."""
+    if x.dim() != 2 or x.dtype != torch.float32 or not x.is_cuda or x.stride(1) != 1:
+        raise ValueError("x must be a float32 [rows, K] tensor with contiguous rows on a HIP device")
+    M, K = x.shape
+    if weight.dtype != torch.float32 or weight.device != x.device or weight.dim() != 2 or weight.size(1) != K \
+            or not weight.is_contiguous():
+        raise ValueError(f"weight must be a contiguous float32 [N, {K}] tensor on {x.device}")
+    N = weight.size(0)
+    if bias is not None and (bias.dtype != torch.float32 or bias.device != x.device or bias.shape != (N,)
+                             or not bias.is_contiguous()):
+        raise ValueError(f"bias must be a contiguous float32 [{N}] tensor on {x.device}")
+    if epilogue not in _EPILOGUES:
+        raise ValueError(f"epilogue must be one of {sorted(_EPILOGUES)}")
+    gamma = beta = None
+    eps = 0.0
+    if ln is not None:
+        gamma, beta, eps = ln
+        for name, t in (("ln weight", gamma), ("ln bias", beta)):
+            if t.dtype != torch.float32 or t.device != x.device or t.shape != (K,) or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous float32 [{K}] tensor on {x.device}")
+    if out is None:
+        if epilogue == "residual":
+            raise ValueError("the residual epilogue adds into out: pass it")
+        out = torch.empty(M, N, dtype=torch.float32, device=x.device)
+    elif out.shape != (M, N) or out.dtype != torch.float32 or out.device != x.device or (M > 1 and out.stride(1) != 1):
+        raise ValueError(f"out must be a float32 [{M}, {N}] tensor with contiguous rows on {x.device}")
+    row = lambda t, w: t.stride(0) if M > 1 else w  # noqa: E731  (a one-row view may carry any stride)
+    st = _lib.lib().tq_skinny_linear(
+        out.data_ptr(), row(out, N), x.data_ptr(), row(x, K), M, weight.data_ptr(),
+        bias.data_ptr() if bias is not None else None, N, K,
+        gamma.data_ptr() if gamma is not None else None, beta.data_ptr() if beta is not None else None,
+        float(eps), _EPILOGUES[epilogue], _stream(x.device),
+    )  # fmt: skip
+    _lib.check(st, "tq_skinny_linear")
+    return out
+
+
+def embed_rows(ids: torch.Tensor, positions: torch.Tensor, wte: torch.Tensor, wpe: torch.Tensor,
+               src: torch.Tensor | None = None, tokens: torch.Tensor | None = None,
+               error_word: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``wte[id] + wpe[pos]`` per row (tokquay/model.py:172), ``id = tokens[src[r]]`` where ``src[r] >= 0``
+    (a token a previous replay left on the device), else ``ids[r]`` (``tq_embed_rows``)."""
+    rows = ids.numel()
+    dev = wte.device
+    V, C = wte.shape
+    for name, t in (("ids", ids), ("positions", positions)) + ((("src", src), ("tokens", tokens)) if src is not None else ()):
+        if t is None or t.dtype != torch.int64 or t.device != dev or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous int64 tensor on {dev}")
+    if positions.numel() != rows or (src is not None and src.numel() != rows):
+        raise ValueError("ids, positions and src need one entry per row")
+    if out is None:
+        out = torch.empty(rows, C, dtype=torch.float32, device=dev)
+    elif out.shape != (rows, C) or out.dtype != torch.float32 or out.device != dev or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous float32 [{rows}, {C}] tensor on {dev}")
+    st = _lib.lib().tq_embed_rows(
+        out.data_ptr(), C, ids.data_ptr(), src.data_ptr() if src is not None else None,
+        tokens.data_ptr() if tokens is not None else None, positions.data_ptr(), wte.data_ptr(), wpe.data_ptr(),
+        rows, C, V, wpe.size(0), error_word.data_ptr() if error_word is not None else None, _stream(dev),
+    )  # fmt: skip
+    _lib.check(st, "tq_embed_rows")
+    return out
