@@ -251,14 +251,21 @@ tq_status tq_add_layernorm(float* x_out, int64_t x_out_stride, float* h_out, int
  * x. Reads W once; the partial products of the K slices are summed in a fixed
  * order (repeated calls give the same bits).
  *
+ * Some shapes (K = 3072 with few columns) split K over several workgroups and need a
+ * workspace of tq_skinny_linear_workspace_size() bytes (0: none), 256-byte
+ * aligned, zeroed once before its first use: each call leaves it ready for the
+ * next. Calls that share a workspace must not run concurrently.
+ *
  * Replaces, for decode steps of at most 16 sequences, the c_attn / c_proj / c_fc
  * / mlp.c_proj linears (tokquay/model.py:62-63, :103-104) with ln_1 / ln_2 in
  * front (:117-118), the GELU (:107) and the residual adds (:122-123), and the
  * LM head with ln_f (:180-181, W = wte, no bias).
  */
+size_t tq_skinny_linear_workspace_size(int32_t M, int32_t N, int32_t K, int32_t has_layernorm);
 tq_status tq_skinny_linear(float* y, int64_t y_stride, const float* x, int64_t x_stride, int32_t M,
                            const float* w, const float* bias, int32_t N, int32_t K, const float* ln_gamma,
-                           const float* ln_beta, float ln_eps, int32_t epilogue, void* stream);
+                           const float* ln_beta, float ln_eps, int32_t epilogue, void* workspace,
+                           size_t workspace_bytes, void* stream);
 
 /*
  * x[r] = wte[id_r] + wpe[positions[r]] for rows r < rows, C columns (a multiple

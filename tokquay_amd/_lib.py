@@ -100,9 +100,11 @@ SIGNATURES: dict[str, tuple] = {
         [
             c_f32p, ctypes.c_int64, c_f32p, ctypes.c_int64, ctypes.c_int32,  # y, y_stride, x, x_stride, M
             c_f32p, c_f32p, ctypes.c_int32, ctypes.c_int32,  # w, bias, N, K
-            c_f32p, c_f32p, ctypes.c_float, ctypes.c_int32, ctypes.c_void_p,  # ln_gamma, ln_beta, ln_eps, epilogue, stream
+            c_f32p, c_f32p, ctypes.c_float, ctypes.c_int32,  # ln_gamma, ln_beta, ln_eps, epilogue
+            ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,  # workspace, workspace_bytes, stream
         ],
     ),
+    "tq_skinny_linear_workspace_size": (ctypes.c_size_t, [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]),
     "tq_embed_rows": (
         ctypes.c_int,
         [

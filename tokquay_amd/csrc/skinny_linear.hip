@@ -20,10 +20,17 @@
 // float4 registers) of 16 R output columns; a workgroup's KW = K / 192 waves cover
 // all of K, and their partial products are summed through LDS in a fixed order.
 // Every load of W is issued before anything waits: block r + 1 while block r is
-// multiplied. (The 768-column layers leave most CUs idle - 48 column blocks - but
-// splitting their K over workgroups costs more than it saves: a cross-XCD
-// reduction needs an L2 write-back per workgroup, and deferring the sum to the
-// next launch makes every one of its workgroups read all the partial products.)
+// multiplied.
+//
+// mlp.c_proj (768 columns, K = 3072) has 48 column blocks, too few for 256 CUs, so
+// its K is split over KSPLIT workgroups per block. Each stores its partial tile with
+// agent-scope atomic stores (written through to the device's coherence point:
+// the XCDs' L2s are not coherent with each other), waits for them to complete,
+// and counts its arrival with an agent-scope atomic add; the last to arrive reads
+// the KSPLIT tiles back with agent-scope atomic loads, sums them in a fixed order
+// (results do not depend on timing), runs the epilogue, and resets the counter
+// for the next launch. No device-wide cache write-back or invalidate is needed,
+// since nothing else the workgroups share travels through the caches.
 //
 // The LayerNorm (whole K in one workgroup) normalises X in registers: two-pass row
 // statistics over the registers, combined across the waves through LDS, with gamma
@@ -44,6 +51,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int kSkinnyRows = 16;
 constexpr int kSkinnyT = 12;                  // float4 steps of 16 k per wave
 constexpr int kSkinnyRange = 16 * kSkinnyT;  // k per wave (one slice)
+constexpr int kSkinnyKSplit = 4;             // workgroups per column block when K is split
 
 enum Epilogue { kEpiBias = 0, kEpiGelu = 1, kEpiResidual = 2 };
 
@@ -56,6 +64,8 @@ struct SkinnyArgs {
   const float* bias;   // may be null
   const float* gamma;  // LayerNorm weight / bias (fused LN only)
   const float* beta;
+  float* partials;    // [blocks][KSPLIT][16][16 R] (split launches)
+  int32_t* arrivals;  // [blocks], zero between launches (split launches)
   float eps;
   int32_t M;
   int32_t N;
@@ -77,13 +87,14 @@ __device__ __forceinline__ void store_output(const SkinnyArgs& a, int m, int n, 
   *yp = v;
 }
 
-template <int KW, int R, bool LN, int EPI>
+template <int KW, int R, bool LN, int EPI, int KSPLIT>
 __global__ __launch_bounds__(kWave* KW) void skinny_linear_kernel(const SkinnyArgs a) {
+  static_assert(!LN || KSPLIT == 1, "the LayerNorm needs every k slice of a row in one workgroup");
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int i = lane & 15;
   const int g = lane >> 4;
-  const int k_lo = wave * kSkinnyRange;
+  const int k_lo = (blockIdx.y * KW + wave) * kSkinnyRange;  // blockIdx.y: the K part (split launches)
   const int n_base = blockIdx.x * (16 * R);
 
   // gamma / beta first (needed first, after the X loads), staged to LDS for the whole K.
@@ -194,42 +205,86 @@ __global__ __launch_bounds__(kWave* KW) void skinny_linear_kernel(const SkinnyAr
 
   // Output o = (m, nn): m = o / (16 R), column n_base + nn. Its value sits in lane m + 16 (c / 4),
   // register c % 4 of block nn / 16, c = nn % 16.
-  for (int o = threadIdx.x; o < 16 * kSkinnyRows * R; o += kWave * KW) {
-    const int m = o / (16 * R);
-    const int nn = o - m * (16 * R);
-    const int n = n_base + nn;
-    if (m >= a.M || n >= a.N) continue;
-    const int c = nn & 15;
-    float v = 0.f;
+  constexpr int kOut = 16 * kSkinnyRows * R;
+  if constexpr (KSPLIT == 1) {
+    for (int o = threadIdx.x; o < kOut; o += kWave * KW) {
+      const int m = o / (16 * R);
+      const int nn = o - m * (16 * R);
+      const int n = n_base + nn;
+      if (m >= a.M || n >= a.N) continue;
+      const int c = nn & 15;
+      float v = 0.f;
 #pragma unroll
-    for (int w = 0; w < KW; ++w) v += part[w][nn >> 4][m + 16 * (c >> 2)][c & 3];
-    store_output<EPI>(a, m, n, v);
+      for (int w = 0; w < KW; ++w) v += part[w][nn >> 4][m + 16 * (c >> 2)][c & 3];
+      store_output<EPI>(a, m, n, v);
+    }
+  } else {
+    float* mine = a.partials + ((int64_t)blockIdx.x * KSPLIT + blockIdx.y) * kOut;
+    for (int o = threadIdx.x; o < kOut; o += kWave * KW) {
+      const int m = o / (16 * R);
+      if (m >= a.M) break;  // rows past the batch are never read
+      const int nn = o - m * (16 * R);
+      const int c = nn & 15;
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < KW; ++w) v += part[w][nn >> 4][m + 16 * (c >> 2)][c & 3];
+      __hip_atomic_store(mine + o, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
+    __syncthreads();                // ... and every thread's
+    __shared__ int s_last;
+    if (threadIdx.x == 0)
+      s_last = __hip_atomic_fetch_add(a.arrivals + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               KSPLIT - 1;
+    __syncthreads();
+    if (!s_last) return;
+    const float* tiles = a.partials + (int64_t)blockIdx.x * KSPLIT * kOut;
+    for (int o = threadIdx.x; o < kOut; o += kWave * KW) {
+      const int m = o / (16 * R);
+      if (m >= a.M) break;
+      const int nn = o - m * (16 * R);
+      const int n = n_base + nn;
+      if (n >= a.N) continue;
+      float v = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < KSPLIT; ++ks)
+        v += __hip_atomic_load(tiles + ks * kOut + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      store_output<EPI>(a, m, n, v);
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(a.arrivals + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
-template <int KW, int R, bool LN>
+template <int KW, int R, bool LN, int KSPLIT = 1>
 void launch_skinny_epi(const SkinnyArgs& a, int epi, hipStream_t s) {
-  const dim3 grid((unsigned)((a.N + 16 * R - 1) / (16 * R))), block(kWave * KW);
+  const dim3 grid((unsigned)((a.N + 16 * R - 1) / (16 * R)), KSPLIT), block(kWave * KW);
   switch (epi) {
-    case kEpiGelu: hipLaunchKernelGGL((skinny_linear_kernel<KW, R, LN, kEpiGelu>), grid, block, 0, s, a); break;
-    case kEpiResidual:
-      hipLaunchKernelGGL((skinny_linear_kernel<KW, R, LN, kEpiResidual>), grid, block, 0, s, a);
+    case kEpiGelu:
+      hipLaunchKernelGGL((skinny_linear_kernel<KW, R, LN, kEpiGelu, KSPLIT>), grid, block, 0, s, a);
       break;
-    default: hipLaunchKernelGGL((skinny_linear_kernel<KW, R, LN, kEpiBias>), grid, block, 0, s, a); break;
+    case kEpiResidual:
+      hipLaunchKernelGGL((skinny_linear_kernel<KW, R, LN, kEpiResidual, KSPLIT>), grid, block, 0, s, a);
+      break;
+    default: hipLaunchKernelGGL((skinny_linear_kernel<KW, R, LN, kEpiBias, KSPLIT>), grid, block, 0, s, a); break;
   }
 }
 
-// Waves per workgroup (K / 192) and column blocks per workgroup for (N, K, LN); {0, 0} when unsupported.
+// Launch shape for (N, K, LN): waves per workgroup, column blocks per workgroup, workgroups per
+// column block (K split); {0, 0, 0} when unsupported.
 struct SkinnyShape {
-  int kw, r;
+  int kw, r, ksplit;
 };
 
 SkinnyShape skinny_shape(int32_t N, int32_t K, bool ln) {
-  if (K % kSkinnyRange != 0) return {0, 0};
+  if (K % kSkinnyRange != 0) return {0, 0, 0};
   const int slices = K / kSkinnyRange;
-  if (slices == 4) return N > 8192 ? SkinnyShape{4, 4} : SkinnyShape{4, 1};  // wide: the LM head
-  if (slices == 16 && !ln) return {16, 1};  // 1024-thread workgroups: one column block fits the registers
-  return {0, 0};
+  const int blocks = (N + 15) / 16;
+  // K = 768: one workgroup per column block (at 768 columns a split costs as much as it saves);
+  // K = 3072 (mlp.c_proj): four workgroups of four slices each per column block.
+  (void)blocks;
+  if (slices == 4) return N > 8192 ? SkinnyShape{4, 4, 1} : SkinnyShape{4, 1, 1};  // wide: the LM head
+  if (slices == 16 && !ln) return {4, 1, kSkinnyKSplit};
+  return {0, 0, 0};
 }
 
 // ------------------------------------------------------------------------------- embeddings
@@ -269,10 +324,20 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(float* x, int64_t x_str
 }  // namespace
 }  // namespace tq
 
+extern "C" size_t tq_skinny_linear_workspace_size(int32_t M, int32_t N, int32_t K, int32_t has_layernorm) {
+  using namespace tq;
+  if (M < 1 || M > kSkinnyRows || N < 1 || K < 1) return 0;
+  const SkinnyShape sh = skinny_shape(N, K, has_layernorm != 0);
+  if (sh.kw == 0 || sh.ksplit == 1) return 0;
+  const int64_t blocks = (N + 16 * sh.r - 1) / (16 * sh.r);
+  const int64_t counters = (blocks * 4 + 255) / 256 * 256;  // arrival counters, then the partial tiles
+  return (size_t)(counters + blocks * sh.ksplit * 16 * kSkinnyRows * sh.r * 4);
+}
+
 extern "C" tq_status tq_skinny_linear(float* y, int64_t y_stride, const float* x, int64_t x_stride, int32_t M,
                                       const float* w, const float* bias, int32_t N, int32_t K,
                                       const float* ln_gamma, const float* ln_beta, float ln_eps, int32_t epilogue,
-                                      void* stream) {
+                                      void* workspace, size_t workspace_bytes, void* stream) {
   using namespace tq;
   if (M < 0 || N < 1 || K < 1 || epilogue < 0 || epilogue > 2) return TQ_ERR_INVALID_ARGUMENT;
   if ((ln_gamma == nullptr) != (ln_beta == nullptr) || (ln_gamma != nullptr && !(ln_eps >= 0.f)))
@@ -295,19 +360,29 @@ extern "C" tq_status tq_skinny_linear(float* y, int64_t y_stride, const float* x
   a.bias = bias;
   a.gamma = ln_gamma;
   a.beta = ln_beta;
+  a.partials = nullptr;
+  a.arrivals = nullptr;
   a.eps = ln_eps;
   a.M = M;
   a.N = N;
   a.K = K;
+  if (sh.ksplit > 1) {
+    const size_t need = tq_skinny_linear_workspace_size(M, N, K, ln ? 1 : 0);
+    if (workspace == nullptr || workspace_bytes < need || (uintptr_t)workspace % 256 != 0)
+      return TQ_ERR_WORKSPACE;
+    const int64_t blocks = (N + 16 * sh.r - 1) / (16 * sh.r);
+    a.arrivals = static_cast<int32_t*>(workspace);
+    a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + (blocks * 4 + 255) / 256 * 256);
+  }
   hipStream_t s = (hipStream_t)stream;
   if (sh.r == 4) {  // wide outputs
     if (ln) launch_skinny_epi<4, 4, true>(a, epilogue, s);
     else launch_skinny_epi<4, 4, false>(a, epilogue, s);
-  } else if (sh.kw == 4) {
+  } else if (sh.ksplit == 1) {
     if (ln) launch_skinny_epi<4, 1, true>(a, epilogue, s);
     else launch_skinny_epi<4, 1, false>(a, epilogue, s);
   } else {
-    launch_skinny_epi<16, 1, false>(a, epilogue, s);
+    launch_skinny_epi<4, 1, false, kSkinnyKSplit>(a, epilogue, s);
   }
   return check_launch();
 }

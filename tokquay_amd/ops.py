@@ -249,6 +249,24 @@ SKINNY_WIDTHS = (768, 3072)
 _EPILOGUES = {"none": 0, "gelu": 1, "residual": 2}
 
 
+_SKINNY_WS_MIN = 1 << 20
+# Per device: tq_skinny_linear's split-K workspace (arrival counters + partial tiles), zeroed once; each
+# call leaves it ready for the next. Buffers live as long as the process: captured graphs hold their
+# addresses.
+_skinny_ws: dict[torch.device, list[torch.Tensor]] = {}
+
+
+def _skinny_workspace(device: torch.device, need: int) -> torch.Tensor | None:
+    if need == 0:
+        return None
+    bufs = _skinny_ws.setdefault(device, [])
+    if not bufs or bufs[-1].numel() < need:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("tq_skinny_linear's workspace must exist before graph capture (run the shape once)")
+        bufs.append(torch.zeros(max(need, _SKINNY_WS_MIN), dtype=torch.uint8, device=device))
+    return bufs[-1]
+
+
 def skinny_supported(rows: int, in_features: int) -> bool:
     """Whether ``tq_skinny_linear`` takes this shape (at most 16 rows, K = 768 or 3072)."""
     return 0 < rows <= SKINNY_MAX_ROWS and in_features in SKINNY_WIDTHS
@@ -288,11 +306,14 @@ def skinny_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | No
     elif out.shape != (M, N) or out.dtype != torch.float32 or out.device != x.device or (M > 1 and out.stride(1) != 1):
         raise ValueError(f"out must be a float32 [{M}, {N}] tensor with contiguous rows on {x.device}")
     row = lambda t, w: t.stride(0) if M > 1 else w  # noqa: E731  (a one-row view may carry any stride)
-    st = _lib.lib().tq_skinny_linear(
+    L = _lib.lib()
+    ws = _skinny_workspace(x.device, int(L.tq_skinny_linear_workspace_size(M, N, K, int(ln is not None))))
+    st = L.tq_skinny_linear(
         out.data_ptr(), row(out, N), x.data_ptr(), row(x, K), M, weight.data_ptr(),
         bias.data_ptr() if bias is not None else None, N, K,
         gamma.data_ptr() if gamma is not None else None, beta.data_ptr() if beta is not None else None,
-        float(eps), _EPILOGUES[epilogue], _stream(x.device),
+        float(eps), _EPILOGUES[epilogue], ws.data_ptr() if ws is not None else None,
+        ws.numel() if ws is not None else 0, _stream(x.device),
     )  # fmt: skip
     _lib.check(st, "tq_skinny_linear")
     return out
