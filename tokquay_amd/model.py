@@ -58,7 +58,13 @@ class MLP(nn.Module):
         self.c_proj = nn.Linear(4 * cfg.n_embd, cfg.n_embd)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self.c_proj(F.gelu(self.c_fc(x), approximate="tanh"))
+        if x.is_cuda:
+            # GELU (tanh form, tokquay/model.py:107) as the GEMM's epilogue on the GPU (hipBLASLt): one launch
+            # instead of two. On the CPU torch's fused path computes the erf form, so it is not used there.
+            h = torch._addmm_activation(self.c_fc.bias, x, self.c_fc.weight.t(), use_gelu=True)
+        else:
+            h = F.gelu(self.c_fc(x), approximate="tanh")
+        return self.c_proj(h)
 
 
 class Block(nn.Module):

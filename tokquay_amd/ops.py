@@ -249,21 +249,23 @@ SKINNY_WIDTHS = (768, 3072)
 _EPILOGUES = {"none": 0, "gelu": 1, "residual": 2}
 
 
-_SKINNY_WS_MIN = 1 << 20
-# Per device: tq_skinny_linear's split-K workspace (arrival counters + partial tiles), zeroed once; each
-# call leaves it ready for the next. Buffers live as long as the process: captured graphs hold their
-# addresses.
-_skinny_ws: dict[torch.device, list[torch.Tensor]] = {}
+_SCRATCH_MIN = 1 << 20
+# Per (device, use): zeroed device buffers that the kernels leave zeroed after every call (split-K arrival
+# counters and partial tiles). Zeroed once; kept for the life of the process, since captured graphs hold
+# their addresses. One per use, so two kernels that may be in flight together never share one.
+_scratch: dict[tuple[torch.device, str], list[torch.Tensor]] = {}
 
 
-def _skinny_workspace(device: torch.device, need: int) -> torch.Tensor | None:
-    if need == 0:
+def zeroed_scratch(device: torch.device, use: str, nbytes: int) -> torch.Tensor | None:
+    """A zero-initialised uint8 buffer of at least ``nbytes`` on ``device`` for ``use`` (None for 0 bytes).
+    Grown only outside graph capture: run a shape once before capturing it."""
+    if nbytes == 0:
         return None
-    bufs = _skinny_ws.setdefault(device, [])
-    if not bufs or bufs[-1].numel() < need:
+    bufs = _scratch.setdefault((torch.device(device), use), [])
+    if not bufs or bufs[-1].numel() < nbytes:
         if torch.cuda.is_current_stream_capturing():
-            raise RuntimeError("tq_skinny_linear's workspace must exist before graph capture (run the shape once)")
-        bufs.append(torch.zeros(max(need, _SKINNY_WS_MIN), dtype=torch.uint8, device=device))
+            raise RuntimeError(f"the {use} buffer must exist before graph capture (run the shape once)")
+        bufs.append(torch.zeros(max(nbytes, _SCRATCH_MIN), dtype=torch.uint8, device=device))
     return bufs[-1]
 
 
@@ -307,7 +309,7 @@ def skinny_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | No
         raise ValueError(f"out must be a float32 [{M}, {N}] tensor with contiguous rows on {x.device}")
     row = lambda t, w: t.stride(0) if M > 1 else w  # noqa: E731  (a one-row view may carry any stride)
     L = _lib.lib()
-    ws = _skinny_workspace(x.device, int(L.tq_skinny_linear_workspace_size(M, N, K, int(ln is not None))))
+    ws = zeroed_scratch(x.device, "skinny linear", int(L.tq_skinny_linear_workspace_size(M, N, K, int(ln is not None))))
     st = L.tq_skinny_linear(
         out.data_ptr(), row(out, N), x.data_ptr(), row(x, K), M, weight.data_ptr(),
         bias.data_ptr() if bias is not None else None, N, K,
@@ -343,3 +345,4 @@ def embed_rows(ids: torch.Tensor, positions: torch.Tensor, wte: torch.Tensor, wp
     )  # fmt: skip
     _lib.check(st, "tq_embed_rows")
     return out
+
