@@ -309,7 +309,9 @@ def skinny_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | No
         raise ValueError(f"out must be a float32 [{M}, {N}] tensor with contiguous rows on {x.device}")
     row = lambda t, w: t.stride(0) if M > 1 else w  # noqa: E731  (a one-row view may carry any stride)
     L = _lib.lib()
-    ws = zeroed_scratch(x.device, "skinny linear", int(L.tq_skinny_linear_workspace_size(M, N, K, int(ln is not None))))
+    # One buffer per (N, K): the split layout (counters, then tiles) depends on the shape.
+    ws = zeroed_scratch(x.device, f"skinny linear {N}x{K}",
+                        int(L.tq_skinny_linear_workspace_size(M, N, K, int(ln is not None))))  # fmt: skip
     st = L.tq_skinny_linear(
         out.data_ptr(), row(out, N), x.data_ptr(), row(x, K), M, weight.data_ptr(),
         bias.data_ptr() if bias is not None else None, N, K,
