@@ -19,8 +19,8 @@
 // Work split: a wave owns one 192-wide k slice (each lane keeps its part of X in 12
 // float4 registers) of 16 R output columns; a workgroup's KW = K / 192 waves cover
 // all of K, and their partial products are summed through LDS in a fixed order.
-// Every load of W is issued before anything waits: block r + 1 while block r is
-// multiplied.
+// Every load of W is issued before anything waits: the first two column blocks at
+// the start, block r + 2 as soon as block r's products have freed its registers.
 //
 // mlp.c_proj (768 columns, K = 3072) has 48 column blocks, too few for 256 CUs, so
 // its K is split over KSPLIT workgroups per block. Each stores its partial tile with
@@ -120,7 +120,7 @@ __global__ __launch_bounds__(kWave* KW) void skinny_linear_kernel(const SkinnyAr
   }
 
   // W rows n_base + 16 r + i; rows past N (the ragged last block) read row N - 1 and are not
-  // stored. Block 0 is issued before anything waits; block r + 1 while block r is multiplied.
+  // stored.
   auto load_w = [&](floatx4 (&wv)[kSkinnyT], int r) {
     const int n = min(n_base + 16 * r + i, a.N - 1);
     const float* wp = a.w + (int64_t)n * a.K + k_lo + 4 * g;
@@ -130,7 +130,8 @@ __global__ __launch_bounds__(kWave* KW) void skinny_linear_kernel(const SkinnyAr
   };
   floatx4 wb[R > 1 ? 2 : 1][kSkinnyT];
   load_w(wb[0], 0);
-  __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of everything below
+  if constexpr (R > 1) load_w(wb[1], 1);  // two column blocks in flight from the start
+  __builtin_amdgcn_sched_barrier(0);       // keep the loads ahead of everything below
 
   if constexpr (LN) {
     if ((int)threadIdx.x < kLnVec) {
@@ -180,10 +181,6 @@ __global__ __launch_bounds__(kWave* KW) void skinny_linear_kernel(const SkinnyAr
   floatx4 acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    if (r + 1 < R) {
-      load_w(wb[(r + 1) & 1], r + 1);
-      __builtin_amdgcn_sched_barrier(0);
-    }
     const floatx4(&wv)[kSkinnyT] = wb[r & 1];
     acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -192,6 +189,11 @@ __global__ __launch_bounds__(kWave* KW) void skinny_linear_kernel(const SkinnyAr
       acc[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][1], xr[t].y, acc[r], 0, 0, 0);
       acc[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][2], xr[t].z, acc[r], 0, 0, 0);
       acc[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][3], xr[t].w, acc[r], 0, 0, 0);
+    }
+    if (r + 2 < R) {  // block r + 2 into the registers block r just freed
+      __builtin_amdgcn_sched_barrier(0);
+      load_w(wb[r & 1], r + 2);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
@@ -282,7 +284,7 @@ SkinnyShape skinny_shape(int32_t N, int32_t K, bool ln) {
   // K = 768: one workgroup per column block (at 768 columns a split costs as much as it saves);
   // K = 3072 (mlp.c_proj): four workgroups of four slices each per column block.
   (void)blocks;
-  if (slices == 4) return N > 8192 ? SkinnyShape{4, 4, 1} : SkinnyShape{4, 1, 1};  // wide: the LM head
+  if (slices == 4) return N > 8192 ? SkinnyShape{4, 2, 1} : SkinnyShape{4, 1, 1};  // wide: the LM head
   if (slices == 16 && !ln) return {4, 1, kSkinnyKSplit};
   return {0, 0, 0};
 }
@@ -375,9 +377,9 @@ extern "C" tq_status tq_skinny_linear(float* y, int64_t y_stride, const float* x
     a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + (blocks * 4 + 255) / 256 * 256);
   }
   hipStream_t s = (hipStream_t)stream;
-  if (sh.r == 4) {  // wide outputs
-    if (ln) launch_skinny_epi<4, 4, true>(a, epilogue, s);
-    else launch_skinny_epi<4, 4, false>(a, epilogue, s);
+  if (sh.r == 2) {  // wide outputs
+    if (ln) launch_skinny_epi<4, 2, true>(a, epilogue, s);
+    else launch_skinny_epi<4, 2, false>(a, epilogue, s);
   } else if (sh.ksplit == 1) {
     if (ln) launch_skinny_epi<4, 1, true>(a, epilogue, s);
     else launch_skinny_epi<4, 1, false>(a, epilogue, s);
