@@ -280,14 +280,53 @@ def test_launch_recorded_timing_events():
 
 
 @pytest.mark.parametrize("block_size", [8, 16])
-@pytest.mark.parametrize("num_seqs", [24, 12, 6, 2])
+@pytest.mark.parametrize("num_seqs", [24, 8, 4, 2])
 def test_prefill_key_split_widths(block_size, num_seqs):
     """The prefill launch splits each query tile's keys over 1, 2, 4 or 8 waves depending on how many
-    tiles there are (4608 / 2304 / 1152 / 384 query tiles -> 1 / 2 / 4 / 8 waves), for the
-    block-size-16 path (one block per key tile) and the generic one; every width must match the
-    reference, with ragged lengths and chunk starts."""
+    tiles there are (4608 / 1536 / 768 / 384 query tiles -> 1 / 2 / 4 / 8 waves), for the
+    block-size-16 path (one block per key tile; software-pipelined up to 4 waves) and the generic
+    one; every width must match the reference, with ragged lengths and chunk starts."""
     rng = random.Random(num_seqs)
     lens = [256] + [rng.randint(100, 256) for _ in range(num_seqs - 1)]
     starts = [rng.choice([0, 0, 100, 300]) for _ in range(num_seqs)]
     sc = Scenario(starts, lens, block_size=block_size, seed=90 + num_seqs)
     check(sc, brute=num_seqs <= 6)
+
+
+@pytest.mark.parametrize("block_size", [8, 16])
+@pytest.mark.parametrize("num_seqs", [3, 40])
+def test_prefill_bad_block_id_is_reported_and_contained(block_size, num_seqs):
+    """A block-table entry outside the pool is reported (TQ_DEVERR_BLOCK_ID); the kernel reads block 0
+    in its place and zeroes it, so the bad sequence's rows stay finite and every other sequence's rows
+    are bit-identical to a launch with a valid table (3 sequences: 8 waves per query tile; 40: 1)."""
+    from tokquay_amd import _lib, ops
+
+    rng = random.Random(70 + num_seqs)
+    lens = [rng.randint(20, 200) for _ in range(num_seqs)]
+    starts = [rng.choice([0, 16, 300]) for _ in range(num_seqs)]
+    need = [cdiv(s + n, block_size) for s, n in zip(starts, lens)]
+    nb = sum(need) + 2
+    pool = torch.randn(nb, 2, 2, 12, block_size, 64, generator=torch.Generator().manual_seed(71)).cuda()
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(72)).tolist()
+    tables = torch.zeros(num_seqs, max(need), dtype=torch.int32)
+    i = 0
+    for b, k in enumerate(need):
+        tables[b, :k] = torch.tensor(perm[i : i + k], dtype=torch.int32)
+        i += k
+    cu = torch.tensor([0] + np.cumsum(lens).tolist(), dtype=torch.int32, device="cuda")
+    st = torch.tensor(starts, dtype=torch.int32, device="cuda")
+    q = torch.randn(sum(lens), 768, generator=torch.Generator().manual_seed(73)).cuda()
+    good = torch.empty_like(q)
+    ops.paged_prefill(good, q, pool, 1, tables.cuda(), cu, st, max(lens))
+    bad_seq = 1
+    bad_tables = tables.clone()
+    bad_tables[bad_seq, need[bad_seq] // 2] = nb + 1000
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    got = torch.full_like(q, float("nan"))
+    ops.paged_prefill(got, q, pool, 1, bad_tables.cuda(), cu, st, max(lens), d_error=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == _lib.DEVERR_BLOCK_ID
+    rows = torch.arange(sum(lens))
+    mine = (rows >= int(cu[bad_seq])) & (rows < int(cu[bad_seq + 1]))
+    assert torch.equal(got[~mine.cuda()], good[~mine.cuda()])
+    assert bool(torch.isfinite(got[mine.cuda()]).all())

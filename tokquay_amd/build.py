@@ -38,6 +38,11 @@ HIPCC_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # MFMA sources and results in VGPRs instead of accumulator registers: the
+    # prefill kernel rescales and reads its accumulators every key tile, and the
+    # AGPR form paid a copy in and out for each access.
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
     "-Wall",
 ]
 

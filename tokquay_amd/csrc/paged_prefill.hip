@@ -19,9 +19,17 @@
 // 16g .. 16g+15 of query j and stores them as four float4.
 //
 // Masking is index arithmetic: query i of sequence b sits at q_start[b] + i
-// and sees keys j <= q_start[b] + i (tokquay/kv_cache.py:208-214). Online
-// softmax keeps one running max per query, shared by its four lane groups
-// (combined with gfx950's cross-row lane swaps, no LDS traffic).
+// and sees keys j <= q_start[b] + i (tokquay/kv_cache.py:208-214); only the
+// tiles that cross the diagonal pay for the compare. Online softmax keeps one
+// running max per query, shared by its four lane groups (combined with gfx950's
+// cross-row lane swaps, no LDS traffic), in log2 units (q is pre-scaled by
+// log2 e, so p = 2^(s - m) on v_exp_f32). The max is lazy: it moves, and the
+// accumulators are rescaled, only when a score passes it by more than 2^8.
+//
+// With block size 16 the key loop is software-pipelined: each wave issues the
+// next key tile's K/V loads before the current tile's math. The MFMA results
+// stay in VGPRs (built with -amdgpu-mfma-vgpr-form), so the per-tile rescale
+// and the softmax read them without accumulator-register copies.
 //
 // Reference semantics: PagedBatch.gather + mask (tokquay/kv_cache.py:208-214,
 // :234-242) and Attention.forward's masked softmax (tokquay/model.py:94-96).
@@ -37,6 +45,8 @@ namespace {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 16;  // queries per wave, keys per step
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kSlack = 8.f;  // log2 units a stale running maximum may trail a score by
 
 struct PrefillArgs {
   float* out;
@@ -215,18 +225,21 @@ __global__ __launch_bounds__(kWave* KS) void prefill_kernel(const PrefillArgs a)
   const int qi = qi0 + j;
   const bool q_ok = qi < nq;
   const int qpos = start + (q_ok ? qi : nq - 1);  // padded lanes mirror the last real query
+  const int qpos_lo = start + qi0;                 // the tile's first query position
 
-  // B operand of the QK product: Q[query j][16g + s], s = 0..15, pre-scaled.
+  // B operand of the QK product: Q[query j][16g + s], s = 0..15, pre-scaled by
+  // scale * log2(e) so the scores come out in log2 units for v_exp_f32.
+  const float qscale = a.scale * kLog2e;
   float qreg[16];
   if (q_ok) {
     const float* qp = a.q + (int64_t)(row0 + qi) * a.q_stride + h * kHeadDim + 16 * g;
 #pragma unroll
     for (int v4 = 0; v4 < 4; ++v4) {
       const float4 x = *reinterpret_cast<const float4*>(qp + 4 * v4);
-      qreg[4 * v4 + 0] = x.x * a.scale;
-      qreg[4 * v4 + 1] = x.y * a.scale;
-      qreg[4 * v4 + 2] = x.z * a.scale;
-      qreg[4 * v4 + 3] = x.w * a.scale;
+      qreg[4 * v4 + 0] = x.x * qscale;
+      qreg[4 * v4 + 1] = x.y * qscale;
+      qreg[4 * v4 + 2] = x.z * qscale;
+      qreg[4 * v4 + 3] = x.w * qscale;
     }
   } else {
 #pragma unroll
@@ -245,15 +258,68 @@ __global__ __launch_bounds__(kWave* KS) void prefill_kernel(const PrefillArgs a)
 
   // Wave w of the workgroup visits key tiles w, w + KS, w + 2 KS, ...: the QK A
   // operand K[kt + j][16g + s] and the PV A operand rows V[kt + 4g + s][4j .. 4j+3].
-  // Block size 16: tile i is block table entry i. The ids of 64 consecutive tiles
-  // are held one per lane and fetched per tile with v_readlane (no table loads in
-  // the loop); the lane copy is refreshed when the wave moves to the next 64.
-  int tb_base = -1;
-  int32_t tb_id = 0;
-  for (int kt = wave * kTile; kt < kend; kt += KS * kTile) {
-    float kreg[16];
-    float4 vreg[4];
-    if constexpr (BS_CT == kTile) {
+  // One key tile's math: S^T = K Q^T, the online-softmax update, O^T += V^T P^T.
+  auto consume = [&](int kt, const float (&kreg)[16], const float4 (&vreg)[4]) {
+      // Two independent MFMA chains (even / odd dim groups) halve the dependent latency.
+      floatx4 st0 = {0.f, 0.f, 0.f, 0.f}, st1 = {0.f, 0.f, 0.f, 0.f};
+  #pragma unroll
+      for (int s = 0; s < 16; s += 2) {
+        st0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kreg[s], qreg[s], st0, 0, 0, 0);
+        st1 = __builtin_amdgcn_mfma_f32_16x16x4f32(kreg[s + 1], qreg[s + 1], st1, 0, 0, 0);
+      }
+      const floatx4 st = st0 + st1;  // st[r] = S^T[key kt + 4g + r][query j], log2 units
+
+      float sm[4];
+      if (kt + kTile - 1 > qpos_lo) {  // uniform: the tile crosses the causal diagonal
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) sm[r] = kt + 4 * g + r <= qpos ? st[r] : -INFINITY;
+      } else {
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) sm[r] = st[r];
+      }
+      float tmax = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
+      tmax = max_over_lane_groups(tmax);
+      // Lazy rescale: the reference maximum m moves only when a score exceeds it by
+      // more than kSlack (log2 units), so p <= 2^kSlack and the accumulators are
+      // rescaled on few tiles. The test is wave-uniform through the ballot.
+      const bool grow = tmax > m + kSlack;  // false while the query has seen no key
+      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+        const float mn = grow ? tmax : m;
+        const float corr = grow ? __builtin_amdgcn_exp2f(m - mn) : 1.f;  // m = -inf: 0
+        l *= corr;
+  #pragma unroll
+        for (int t = 0; t < 4; ++t) o[t] *= corr;
+        m = mn;
+      }
+      // A query with no visible key so far (m = -inf) has only -inf scores here:
+      // any finite reference gives p = 0 and keeps its state exactly zero.
+      const float mref = m == -INFINITY ? 0.f : m;
+      float p[4];
+  #pragma unroll
+      for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(sm[r] - mref);
+      l += (p[0] + p[1]) + (p[2] + p[3]);
+
+  #pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        o[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(vreg[s].x, p[s], o[0], 0, 0, 0);
+        o[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(vreg[s].y, p[s], o[1], 0, 0, 0);
+        o[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(vreg[s].z, p[s], o[2], 0, 0, 0);
+        o[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vreg[s].w, p[s], o[3], 0, 0, 0);
+      }
+  };
+
+  if constexpr (BS_CT == kTile && KS <= 4) {
+    // Block size 16 and at most 4 waves per workgroup: tile i is block table entry i.
+    // The ids of 64 consecutive tiles are held one per lane and fetched per tile with
+    // v_readlane (no table loads in the loop); the lane copy is refreshed when the
+    // wave moves to the next 64.
+    // The loop is software-pipelined over two register buffers: the next tile's
+    // K/V loads are issued before the current tile's math. Loads are unconditional
+    // (a tile is one whole block, so every address is inside it; a bad id reads
+    // block 0); keys past kend or in a bad block are zeroed after they arrive.
+    int tb_base = -1;
+    int32_t tb_id = 0;
+    auto fetch = [&](int kt, float (&kreg)[16], float4 (&vreg)[4]) -> int32_t {
       const int ti = kt / kTile;
       if ((ti & ~63) != tb_base) {  // wave-uniform
         tb_base = ti & ~63;
@@ -265,53 +331,84 @@ __global__ __launch_bounds__(kWave* KS) void prefill_kernel(const PrefillArgs a)
           else flag_error(a.d_error, TQ_DEVERR_BLOCK_ID);
         }
       }
-      const int64_t blk = __builtin_amdgcn_readlane(tb_id, ti - tb_base);
-      load_kv_block_tile(a, head_base, blk, kt, kend, j, g, kreg, vreg);
-    } else {
-      load_kv_tile<BS_CT>(a, bt, head_base, bs, kt, kend, j, g, kreg, vreg);
+      const int32_t blk = __builtin_amdgcn_readlane(tb_id, ti - tb_base);
+      const float* base = head_base + (int64_t)(blk < 0 ? 0 : blk) * a.block_stride;
+      const float* kp = base + j * kHeadDim + 16 * g;
+#pragma unroll
+      for (int v4 = 0; v4 < 4; ++v4) {
+        const float4 x = *reinterpret_cast<const float4*>(kp + 4 * v4);
+        kreg[4 * v4 + 0] = x.x;
+        kreg[4 * v4 + 1] = x.y;
+        kreg[4 * v4 + 2] = x.z;
+        kreg[4 * v4 + 3] = x.w;
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        vreg[s] = *reinterpret_cast<const float4*>(base + a.kv_stride + (4 * g + s) * kHeadDim + 4 * j);
+      return blk;
+    };
+    // Zero what must not count (uniform test; only the last tile or a bad block).
+    auto mask = [&](int kt, int32_t blk, float (&kreg)[16], float4 (&vreg)[4]) {
+      if (blk < 0 || kt + kTile > kend) {
+        const bool k_ok = blk >= 0 && kt + j < kend;
+#pragma unroll
+        for (int s = 0; s < 16; ++s) kreg[s] = k_ok ? kreg[s] : 0.f;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const bool v_ok = blk >= 0 && kt + 4 * g + s < kend;
+          vreg[s] = v_ok ? vreg[s] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+    };
+    const int step = KS * kTile;
+    int kt = wave * kTile;
+    if (kt < kend) {
+      float ka[16], kb[16];
+      float4 va[4], vb[4];
+      int32_t ba = fetch(kt, ka, va), bb;
+      while (true) {
+        // Always issue the next loads (the last tile re-reads itself), so the wait
+        // counts before each tile's math are the same on every path.
+        const bool more = kt + step < kend;  // uniform
+        bb = fetch(more ? kt + step : kt, kb, vb);
+        __builtin_amdgcn_sched_barrier(0);
+        mask(kt, ba, ka, va);
+        consume(kt, ka, va);
+        if (!more) break;
+        kt += step;
+        const bool more2 = kt + step < kend;
+        ba = fetch(more2 ? kt + step : kt, ka, va);
+        __builtin_amdgcn_sched_barrier(0);
+        mask(kt, bb, kb, vb);
+        consume(kt, kb, vb);
+        if (!more2) break;
+        kt += step;
+      }
     }
-    // Two independent MFMA chains (even / odd dim groups) halve the dependent latency.
-    floatx4 st0 = {0.f, 0.f, 0.f, 0.f}, st1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < 16; s += 2) {
-      st0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kreg[s], qreg[s], st0, 0, 0, 0);
-      st1 = __builtin_amdgcn_mfma_f32_16x16x4f32(kreg[s + 1], qreg[s + 1], st1, 0, 0, 0);
-    }
-    const floatx4 st = st0 + st1;  // st[r] = S^T[key kt + 4g + r][query j]
-
-    float sm[4];
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int key = kt + 4 * g + r;
-      sm[r] = key <= qpos ? st[r] : -INFINITY;
-      tmax = fmaxf(tmax, sm[r]);
-    }
-    tmax = max_over_lane_groups(tmax);
-    const float mn = fmaxf(m, tmax);
-    // A wave whose tiles start past a query's position has seen no visible key
-    // for it yet (mn = -inf): any finite reference keeps its state exactly zero
-    // (corr = exp(-inf) = 0, every p = 0) without a divergent branch.
-    const float mref = mn == -INFINITY ? 0.f : mn;
-    const float corr = __expf(m - mref);
-    float p[4];
-    float ps = 0.f;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      p[r] = sm[r] == -INFINITY ? 0.f : __expf(sm[r] - mref);
-      ps += p[r];
-    }
-    l = fmaf(l, corr, ps);
-    m = mn;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) o[t] *= corr;
-
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      o[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(vreg[s].x, p[s], o[0], 0, 0, 0);
-      o[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(vreg[s].y, p[s], o[1], 0, 0, 0);
-      o[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(vreg[s].z, p[s], o[2], 0, 0, 0);
-      o[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vreg[s].w, p[s], o[3], 0, 0, 0);
+  } else {
+    int tb_base = -1;
+    int32_t tb_id = 0;
+    for (int kt = wave * kTile; kt < kend; kt += KS * kTile) {
+      float kreg[16];
+      float4 vreg[4];
+      if constexpr (BS_CT == kTile) {
+        const int ti = kt / kTile;
+        if ((ti & ~63) != tb_base) {  // wave-uniform
+          tb_base = ti & ~63;
+          const int nblk = (kend + kTile - 1) / kTile;
+          tb_id = -1;
+          if (tb_base + lane < nblk) {
+            const int32_t id = bt[tb_base + lane];
+            if ((uint32_t)id < (uint32_t)a.num_blocks) tb_id = id;
+            else flag_error(a.d_error, TQ_DEVERR_BLOCK_ID);
+          }
+        }
+        const int64_t blk = __builtin_amdgcn_readlane(tb_id, ti - tb_base);
+        load_kv_block_tile(a, head_base, blk, kt, kend, j, g, kreg, vreg);
+      } else {
+        load_kv_tile<BS_CT>(a, bt, head_base, bs, kt, kend, j, g, kreg, vreg);
+      }
+      consume(kt, kreg, vreg);
     }
   }
 
@@ -352,7 +449,7 @@ __global__ __launch_bounds__(kWave* KS) void prefill_kernel(const PrefillArgs a)
 #pragma unroll
       for (int w = 0; w < KS; ++w) {
         const float mw = s_ml[w][0][j];
-        const float cw = mw == -INFINITY ? 0.f : __expf(mw - M);  // waves that saw no key weigh 0
+        const float cw = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);  // waves that saw no key weigh 0
         L = fmaf(s_ml[w][1][j], cw, L);
         acc.x = fmaf(s_o[w][lane][4 * part + 0], cw, acc.x);
         acc.y = fmaf(s_o[w][lane][4 * part + 1], cw, acc.y);
@@ -377,13 +474,21 @@ void launch_prefill_ks(const PrefillArgs& a, hipStream_t stream, hipEvent_t star
                           stop, 0, a);
 }
 
-// Waves per workgroup: double the key split while the (sequence, head, query tile)
-// work items times KS give fewer than three waves per SIMD of the 256 CUs, up to 8
-// (measured on 256-token chunks: 768 tiles run best with 4, 576 tiles with 8).
+// Waves per workgroup: the largest key split KS that still lets every workgroup of
+// the launch be resident at once (a second round of workgroups costs more than the
+// split saves). The pipelined kernel (KS <= 4) holds 3 waves per SIMD, so a CU
+// takes 12 / KS of its workgroups: KS = 4 up to 768 tiles, 2 up to 1536. The KS = 8
+// instance runs the plain loop at 5 waves per SIMD, two workgroups per CU: up to
+// 512 tiles. Measured on 256-token chunks: 768 tiles run best with 4, 960 with 2,
+// 576 with 4; KS = 16 on 192-252 tiles ran 15-20 % slower than 8.
 int choose_key_split(int64_t tiles) {
-  int ks = 1;
-  while (ks < 8 && tiles * ks < 3072) ks *= 2;
-  return ks;
+  constexpr int kCus = 256;
+  constexpr int kSlotsPlain = 20;      // wave slots per CU at 5 waves per SIMD
+  constexpr int kSlotsPipelined = 12;  // at 3 waves per SIMD
+  if (tiles <= (int64_t)kCus * (kSlotsPlain / 8)) return 8;
+  for (int ks = 4; ks > 1; ks /= 2)
+    if (tiles <= (int64_t)kCus * (kSlotsPipelined / ks)) return ks;
+  return 1;
 }
 
 template <int BS_CT>
