@@ -77,30 +77,32 @@ struct PrefillArgs {
 constexpr int kXcds = 8;      // MI355X: workgroup i is dispatched to XCD i % 8
 constexpr int kRound = 64;    // dispatches per XCD taken as one round (two per CU of its 32)
 
-// Maps the dispatch index to a work tile. The (sequence, head) groups are dealt out
-// whole to the XCDs (workgroup p runs on XCD p % 8), so all query tiles of a group
-// share one L2 for their K/V reads; an XCD with one group fewer than the largest
-// gets padding workgroups that exit at once. Inside an XCD the tiles go out by cost
-// (query tile index, descending across its G groups) and the rounds of kRound
-// dispatches snake: round k even takes cost ranks k kRound .. k kRound + kRound - 1
-// in order, odd in reverse, so the tiles a CU receives over two rounds add up to
-// about the same number of key tiles (measured on 256-token chunks of 4 prompts:
-// 15.1 / 24.9 / 34.5 -> 11.5 / 21.5 / 31.4 us at starts 0 / 256 / 512 against
-// contiguous runs with the last query tiles first; rounds of 32 or 128 do about as
-// well, 16 worse). Returns false for a padding workgroup.
+// Maps the dispatch index to a work tile. Workgroup p runs on XCD p % 8 (checked
+// on MI355X with the XCC_ID register), and the XCD hands its workgroups to its 32
+// CUs round robin. The (sequence, head) groups are dealt out whole, group g to XCD
+// g % 8, so all query tiles of a group share one L2 for their K/V reads and the
+// heads of a long sequence spread over all eight XCDs; an XCD with one group fewer
+// than the most gets padding workgroups that exit at once. Inside an XCD the tiles
+// go out by cost (query tile index, descending across its G groups) and the rounds
+// of kRound dispatches snake: round k even takes cost ranks k kRound .. k kRound +
+// kRound - 1 in order, odd in reverse, so the tiles a CU receives over two rounds
+// add up to about the same number of key tiles (measured on 256-token chunks of 4
+// prompts: 15.1 / 24.9 / 34.5 -> 11.5 / 21.5 / 31.4 us at starts 0 / 256 / 512
+// against contiguous runs with the last query tiles first; rounds of 32 or 128 do
+// about as well, 16 worse; dealing contiguous runs of groups instead of every
+// eighth group left a 3-prompt chunk with one long prompt 45 % slower). Returns
+// false for a padding workgroup.
 __device__ __forceinline__ bool tile_of(const PrefillArgs& a, int& qt, int& h, int& b) {
   const int p = blockIdx.x;
   const int xcd = p % kXcds, local = p / kXcds;
-  const int gq = a.groups / kXcds, gr = a.groups % kXcds;
-  const int G = gq + (xcd < gr ? 1 : 0);   // groups on this XCD
-  const int g0 = xcd * gq + min(xcd, gr);  // its first group
+  const int G = (a.groups - xcd + kXcds - 1) / kXcds;  // groups xcd, xcd + 8, ... on this XCD
   const int n = G * a.qtiles;
   if (local >= n) return false;
   const int k = local / kRound, c = local - k * kRound;
   const int m = min(kRound, n - k * kRound);  // size of this round
   const int rank = k * kRound + ((k & 1) ? m - 1 - c : c);
   qt = a.qtiles - 1 - rank / G;
-  const int seq_head = g0 + rank % G;
+  const int seq_head = xcd + kXcds * (rank % G);
   h = seq_head % a.num_heads;
   b = seq_head / a.num_heads;
   return true;
@@ -465,12 +467,20 @@ __global__ __launch_bounds__(kWave* KS) void prefill_kernel(const PrefillArgs a)
   }
 }
 
+// The 8-wave instance reserves this much extra (unused) LDS per workgroup so that a
+// CU holds only one of them: the round-robin dispatcher otherwise put a second busy
+// workgroup on a CU whose first one was still running while other CUs sat idle
+// (empty query tiles of short sequences in between shift the rotation). A 3-prompt
+// tail chunk with 5 / 102 / 9 rows at position 768: 22.2 -> 14.5 us.
+constexpr size_t kLdsOneGroupPerCu = 64 * 1024;
+
 template <int BS_CT, int KS>
 void launch_prefill_ks(const PrefillArgs& a, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+  const size_t lds = KS == 8 ? kLdsOneGroupPerCu : 0;
   if (start == nullptr && stop == nullptr)
-    hipLaunchKernelGGL((prefill_kernel<BS_CT, KS>), dim3((unsigned)a.total), dim3(kWave * KS), 0, stream, a);
+    hipLaunchKernelGGL((prefill_kernel<BS_CT, KS>), dim3((unsigned)a.total), dim3(kWave * KS), lds, stream, a);
   else
-    hipExtLaunchKernelGGL((prefill_kernel<BS_CT, KS>), dim3((unsigned)a.total), dim3(kWave * KS), 0, stream, start,
+    hipExtLaunchKernelGGL((prefill_kernel<BS_CT, KS>), dim3((unsigned)a.total), dim3(kWave * KS), lds, stream, start,
                           stop, 0, a);
 }
 
@@ -478,14 +488,13 @@ void launch_prefill_ks(const PrefillArgs& a, hipStream_t stream, hipEvent_t star
 // the launch be resident at once (a second round of workgroups costs more than the
 // split saves). The pipelined kernel (KS <= 4) holds 3 waves per SIMD, so a CU
 // takes 12 / KS of its workgroups: KS = 4 up to 768 tiles, 2 up to 1536. The KS = 8
-// instance runs the plain loop at 5 waves per SIMD, two workgroups per CU: up to
-// 512 tiles. Measured on 256-token chunks: 768 tiles run best with 4, 960 with 2,
-// 576 with 4; KS = 16 on 192-252 tiles ran 15-20 % slower than 8.
+// instance runs the plain loop, one workgroup per CU: up to 256 tiles. Measured on
+// 256-token chunks: 768 tiles run best with 4, 960 with 2, 576 with 4; KS = 16 on
+// 192-252 tiles ran 15-20 % slower than 8.
 int choose_key_split(int64_t tiles) {
   constexpr int kCus = 256;
-  constexpr int kSlotsPlain = 20;      // wave slots per CU at 5 waves per SIMD
-  constexpr int kSlotsPipelined = 12;  // at 3 waves per SIMD
-  if (tiles <= (int64_t)kCus * (kSlotsPlain / 8)) return 8;
+  constexpr int kSlotsPipelined = 12;  // wave slots per CU at 3 waves per SIMD
+  if (tiles <= kCus) return 8;
   for (int ks = 4; ks > 1; ks /= 2)
     if (tiles <= (int64_t)kCus * (kSlotsPipelined / ks)) return ks;
   return 1;
