@@ -47,6 +47,7 @@ constexpr int kChunksPerIter = 2;  // chunks whose loads are issued together
 constexpr int kChunk = 16;         // positions per chunk
 constexpr int kPartialStride = kHeadDim + 4;    // acc[64], m, l, 2 pad: 16-byte aligned rows
 constexpr int kMaxPartition = 1024;             // a partition spans <= 64 blocks of >= 16 positions
+constexpr int kCuStratum = 256;                 // MI355X CUs: one dispatch per CU per stratum
 
 struct DecodeArgs {
   float* out;
@@ -259,14 +260,30 @@ __device__ __forceinline__ void consume_chunk(const float4 q4, const float4 (&kx
 template <int BS_CT, bool WRITE>
 __global__ __launch_bounds__(kWave* kHeadsPerGroup) void decode_partition_kernel(const DecodeArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int h = blockIdx.x * kHeadsPerGroup + (threadIdx.x / kWave);
-  const int part = blockIdx.y;
+  // Workgroup p runs on XCD p % 8 and each XCD deals its workgroups to its 32 CUs round
+  // robin, so dispatches 256 s .. 256 s + 255 put one workgroup on every CU. With the
+  // longest contexts listed first, reversing every other such stratum gives each CU
+  // long and short items in turn instead of the longest of every stratum to the same
+  // CUs (measured at 256 sequences, contexts U[256,1024]: 153 -> 151 us per launch).
+  int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+  {
+    const int gx = gridDim.x, gy = gridDim.y;
+    const int total = gx * gy * (int)gridDim.z;
+    int idx = bx + gx * (by + gy * bz);
+    const int s = idx / kCuStratum;
+    if (s & 1) idx = s * kCuStratum + min(kCuStratum, total - s * kCuStratum) - 1 - (idx - s * kCuStratum);
+    bx = idx % gx;
+    by = (idx / gx) % gy;
+    bz = idx / (gx * gy);
+  }
+  const int h = bx * kHeadsPerGroup + (threadIdx.x / kWave);
+  const int part = by;
   if (h >= a.num_heads) return;  // whole wave leaves; the kernel has no barriers
   // Workgroups are dispatched in grid order and older waves win arbitration, so a caller
   // that lists the longest contexts first shortens the tail of the launch.
-  int b = blockIdx.z;
+  int b = bz;
   if (a.seq_order != nullptr) {
-    b = a.seq_order[blockIdx.z];
+    b = a.seq_order[bz];
     if ((uint32_t)b >= (uint32_t)a.num_seqs) {
       if (h == 0 && part == 0 && lane == 0) flag_error(a.d_error, TQ_DEVERR_ORDER);
       return;
