@@ -20,7 +20,6 @@ from dataclasses import dataclass
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
 from tokquay_amd import ops
 from tokquay_amd.kv_cache import PagedBatch
@@ -48,7 +47,7 @@ class Attention(nn.Module):
 
     def forward(self, x: torch.Tensor, cache: PagedBatch, layer: int) -> torch.Tensor:
         # x: [N, C] packed rows. c_attn gives [N, 3C] = [q | k | v], heads contiguous in each.
-        return self.c_proj(cache.attend(layer, self.c_attn(x)))
+        return ops.linear(cache.attend(layer, ops.linear(x, self.c_attn)), self.c_proj)
 
 
 class MLP(nn.Module):
@@ -58,13 +57,9 @@ class MLP(nn.Module):
         self.c_proj = nn.Linear(4 * cfg.n_embd, cfg.n_embd)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if x.is_cuda:
-            # GELU (tanh form, tokquay/model.py:107) as the GEMM's epilogue on the GPU (hipBLASLt): one launch
-            # instead of two. On the CPU torch's fused path computes the erf form, so it is not used there.
-            h = torch._addmm_activation(self.c_fc.bias, x, self.c_fc.weight.t(), use_gelu=True)
-        else:
-            h = F.gelu(self.c_fc(x), approximate="tanh")
-        return self.c_proj(h)
+        # GELU (tanh form, tokquay/model.py:107) as the GEMM's epilogue on the GPU (hipBLASLt): one launch
+        # instead of two. On the CPU torch's fused path computes the erf form, so ops.linear applies it apart.
+        return ops.linear(ops.linear(x, self.c_fc, gelu=True), self.c_proj)
 
 
 class Block(nn.Module):

@@ -348,3 +348,70 @@ def embed_rows(ids: torch.Tensor, positions: torch.Tensor, wte: torch.Tensor, wp
     _lib.check(st, "tq_embed_rows")
     return out
 
+
+
+# ------------------------------------------------------------------------------ library GEMMs
+# hipBLASLt's default fp32 kernel for a given shape depends on the operand layout, and for some
+# row counts the transposed-weight ("NN") call is clearly faster: at 256 rows, c_attn
+# ([768] -> [2304]) 15.8 -> 12.8 us and c_fc (+ GELU, [768] -> [3072]) 16.7 -> 13.7 us, while at
+# 224 or 320 rows, and for the [3072] -> [768] projection at any, the weight as stored ("TN") is
+# as fast or faster. Which layout a launch uses is therefore measured on the device, once per
+# (rows, out, in, epilogue), for the power-of-two row counts decode steps are captured at.
+_gemm_nn: dict[tuple[int, int, int, bool], bool] = {}
+
+
+def _gemm(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, gelu: bool) -> torch.Tensor:
+    if gelu:
+        return torch._addmm_activation(bias, x, w, use_gelu=True)
+    return torch.addmm(bias, x, w) if bias is not None else x @ w
+
+
+def _nn_is_faster(x: torch.Tensor, weight: torch.Tensor, weight_t: torch.Tensor, bias, gelu: bool) -> bool:
+    """Times both layouts (2 warm-up + 5 timed calls each, HIP events on the current stream)."""
+    times = []
+    for w in (weight.t(), weight_t):
+        for _ in range(2):
+            _gemm(x, w, bias, gelu)
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(5):
+            _gemm(x, w, bias, gelu)
+        stop.record()
+        stop.synchronize()
+        times.append(start.elapsed_time(stop))
+    return times[1] < 0.95 * times[0]
+
+
+def transposed_weight(linear: torch.nn.Linear) -> torch.Tensor:
+    """A contiguous ``[in, out]`` copy of ``linear.weight``, kept on the module and rebuilt when the
+    weight's storage or version changes."""
+    w = linear.weight
+    key = (w.data_ptr(), w._version, w.device)
+    cached = getattr(linear, "_tq_weight_t", None)
+    if cached is None or cached[0] != key:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("the transposed weight must exist before graph capture (run the shape once)")
+        cached = (key, w.detach().t().contiguous())
+        linear._tq_weight_t = cached
+    return cached[1]
+
+
+def linear(x: torch.Tensor, layer: torch.nn.Linear, gelu: bool = False) -> torch.Tensor:
+    """``x @ layer.weight.T + layer.bias`` (then the tanh GELU when ``gelu``) through hipBLASLt,
+    in whichever weight layout measured faster for this shape (see above). On the CPU: torch's
+    ``F.linear`` and the tanh GELU."""
+    if not x.is_cuda:
+        y = torch.nn.functional.linear(x, layer.weight, layer.bias)
+        return torch.nn.functional.gelu(y, approximate="tanh") if gelu else y
+    rows = x.shape[0]
+    out_f, in_f = layer.weight.shape
+    key = (rows, out_f, in_f, gelu)
+    use_nn = _gemm_nn.get(key)
+    if use_nn is None:
+        use_nn = False
+        # Measured only for power-of-two row counts of at least 64 (the decode graph buckets),
+        # never while a graph is being captured; other shapes use the stored layout.
+        if rows >= 64 and rows & (rows - 1) == 0 and not torch.cuda.is_current_stream_capturing():
+            use_nn = _gemm_nn[key] = _nn_is_faster(x, layer.weight, transposed_weight(layer), layer.bias, gelu)
+    w = transposed_weight(layer) if use_nn else layer.weight.t()
+    return _gemm(x, w, layer.bias, gelu)
