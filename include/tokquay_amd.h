@@ -13,7 +13,7 @@
  *
  *   tq_argmax_rows    index of each logit row's maximum (greedy sampling)
  *   tq_add_layernorm  residual add fused with the LayerNorm that follows it
- *   tq_skinny_linear  linear layer of at most 16 rows, LayerNorm / bias / GELU /
+ *   tq_skinny_linear  linear layer of at most 64 rows, LayerNorm / bias / GELU /
  *                     residual add fused in (small-batch decode steps)
  *   tq_embed_rows     token + position embeddings of each row
  *
@@ -245,7 +245,7 @@ tq_status tq_add_layernorm(float* x_out, int64_t x_out_stride, float* h_out, int
  *   epilogue 0: y = v;  1: y = gelu_tanh(v);  2: y = y + v (residual add, in place)
  *
  * x [M, K] (row stride x_stride), W [N, K] contiguous (nn.Linear's [out, in]),
- * y [M, N] (row stride y_stride), all fp32. M <= 16; K = 768, or K = 3072 without
+ * y [M, N] (row stride y_stride), all fp32. M <= 64; K = 768, or K = 3072 without
  * the LayerNorm (GPT-2's widths; other shapes return TQ_ERR_UNSUPPORTED); x, W,
  * ln_gamma, ln_beta 16-byte aligned, x_stride a multiple of 4. y must not overlap
  * x. Reads W once; the partial products of the K slices are summed in a fixed
@@ -256,7 +256,7 @@ tq_status tq_add_layernorm(float* x_out, int64_t x_out_stride, float* h_out, int
  * aligned, zeroed once before its first use: each call leaves it ready for the
  * next. Calls that share a workspace must not run concurrently.
  *
- * Replaces, for decode steps of at most 16 sequences, the c_attn / c_proj / c_fc
+ * Replaces, for decode steps of up to 32 sequences (the kernel takes 64), the c_attn / c_proj / c_fc
  * / mlp.c_proj linears (tokquay/model.py:62-63, :103-104) with ln_1 / ln_2 in
  * front (:117-118), the GELU (:107) and the residual adds (:122-123), and the
  * LM head with ln_f (:180-181, W = wte, no bias).

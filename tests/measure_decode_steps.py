@@ -77,7 +77,7 @@ def main() -> None:
         t = step_times(eng)
         print(json.dumps({"sequences": args.profile, "steps": len(t) + 10, "step_p50_ms": round(statistics.median(t) * 1e3, 3)}))
         return
-    for nseq in (1, 8, 16, 64, 256):
+    for nseq in (1, 8, 16, 24, 32, 64, 256):
         row = {"sequences": nseq}
         for mode in MODES:
             row[f"{mode}_p50_ms"] = round(statistics.median(step_times(engine(m, nseq, mode))) * 1e3, 3)

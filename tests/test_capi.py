@@ -98,7 +98,7 @@ def test_decode_workspace_size(lib):
 def test_small_batch_entries_reject_bad_shapes_before_any_launch(lib):
     # tq_skinny_linear(y, y_stride, x, x_stride, M, w, bias, N, K, ln_gamma, ln_beta, ln_eps, epilogue, stream)
     f = lambda *a: lib.tq_skinny_linear(*a, None, 0, None)  # noqa: E731
-    assert f(None, 8, None, 768, 17, None, None, 8, 768, None, None, 0.0, 0) == 2  # M > 16
+    assert f(None, 8, None, 768, 65, None, None, 8, 768, None, None, 0.0, 0) == 2  # M > 64
     assert f(None, 8, None, 512, 2, None, None, 8, 512, None, None, 0.0, 0) == 2  # K
     assert f(None, 8, None, 768, 2, None, None, 8, 768, None, None, 0.0, 3) == 1  # epilogue
     assert f(None, 8, None, 768, 0, None, None, 8, 768, None, None, 0.0, 0) == 0  # no rows
@@ -108,7 +108,8 @@ def test_small_batch_entries_reject_bad_shapes_before_any_launch(lib):
     assert f(4096, 768, 4096, 3072, 2, 4096, None, 768, 3072, None, None, 0.0, 2) == 3
     ws = lib.tq_skinny_linear_workspace_size
     assert ws(16, 2304, 768, 1) == 0 and ws(16, 768, 768, 0) == 0 and ws(16, 768, 3072, 0) > 0
-    assert ws(16, 768, 3072, 1) == 0 and ws(17, 768, 768, 0) == 0  # unsupported shapes
+    assert ws(64, 768, 3072, 0) > ws(33, 768, 3072, 0) > ws(16, 768, 3072, 0)  # partial tiles per row block
+    assert ws(16, 768, 3072, 1) == 0 and ws(65, 768, 3072, 0) == 0  # unsupported shapes
     # tq_embed_rows(x, x_stride, ids, src, tokens, positions, wte, wpe, rows, C, vocab, n_positions, d_error, stream)
     assert lib.tq_embed_rows(None, 768, None, None, None, None, None, None, 0, 768, 10, 10, None, None) == 0
     assert lib.tq_embed_rows(None, 768, None, None, None, None, None, None, 3, 766, 10, 10, None, None) == 2

@@ -1,7 +1,7 @@
-// Linear layers of small decode batches (at most 16 rows), with the LayerNorm in
+// Linear layers of small decode batches (at most 64 rows), with the LayerNorm in
 // front of them and the bias / GELU / residual add after them fused in:
 //
-//   y = epilogue( LN(x) W^T + b )      x [M, K], W [N, K] (nn.Linear layout), M <= 16
+//   y = epilogue( LN(x) W^T + b )      x [M, K], W [N, K] (nn.Linear layout), M <= 64
 //
 // At a few rows a linear layer is a weight stream: every weight is used M times,
 // so the launch is bound by reading W from HBM once, and by latency. The library
@@ -10,17 +10,19 @@
 // them. This kernel makes each linear layer one launch that reads W once.
 //
 // Y^T[n][m] = sum_k W[n][k] X[m][k] on v_mfma_f32_16x16x4_f32: the A operand is 16
-// rows of W, the B operand X^T, so one MFMA block covers the whole batch (rows past M
-// are zero). Lane (i, g) = (lane % 16, lane / 16) loads W[n0 + i][k .. k + 3] and
-// X[i][k .. k + 3] with k = kb + 4 g as float4s; step j = 0..3 of the block then
-// takes component j, so lane group g supplies k = kb + 4 g + j to both operands.
-// The accumulator's lane (j, g) holds Y^T[n0 + 4 g + r][m = j], r = 0..3.
+// rows of W, the B operand X^T, so one MFMA block covers a row block of 16 batch rows
+// (rows past M are zero); up to four row blocks share each W register. Lane (i, g) =
+// (lane % 16, lane / 16) loads W[n0 + i][k .. k + 3] and X[16 mb + i][k .. k + 3] with
+// k = kb + 4 g as float4s; step j = 0..3 of the block then takes component j, so lane
+// group g supplies k = kb + 4 g + j to both operands. The accumulator's lane (j, g)
+// holds Y^T[n0 + 4 g + r][m = 16 mb + j], r = 0..3.
 //
-// Work split: a wave owns one 192-wide k slice (each lane keeps its part of X in 12
-// float4 registers) of 16 R output columns; a workgroup's KW = K / 192 waves cover
-// all of K, and their partial products are summed through LDS in a fixed order.
-// Every load of W is issued before anything waits: the first two column blocks at
-// the start, block r + 2 as soon as block r's products have freed its registers.
+// Work split: a wave owns one k slice (each lane keeps its part of X in registers:
+// 12 float4 per row block for 192-wide slices at up to 32 rows, 6 for 96-wide slices
+// at up to 64) of 16 R output columns; a workgroup's waves cover 768 of K, and their
+// partial products are summed through LDS in a fixed order. Every load of W is issued
+// before anything waits: the first two column blocks at the start, block r + 2 as
+// soon as block r's products have freed its registers.
 //
 // mlp.c_proj (768 columns, K = 3072) has 48 column blocks, too few for 256 CUs, so
 // its K is split over KSPLIT workgroups per block. Each stores its partial tile with
@@ -48,10 +50,9 @@ namespace {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int kSkinnyRows = 16;
-constexpr int kSkinnyT = 12;                  // float4 steps of 16 k per wave
-constexpr int kSkinnyRange = 16 * kSkinnyT;  // k per wave (one slice)
-constexpr int kSkinnyKSplit = 4;             // workgroups per column block when K is split
+constexpr int kSkinnyRows = 16;       // rows of one row block (the MFMA's B columns)
+constexpr int kSkinnyMaxBlocks = 4;   // row blocks: at most 64 rows
+constexpr int kSkinnyKSplit = 4;      // workgroups per column block when K is split
 
 enum Epilogue { kEpiBias = 0, kEpiGelu = 1, kEpiResidual = 2 };
 
@@ -87,19 +88,25 @@ __device__ __forceinline__ void store_output(const SkinnyArgs& a, int m, int n, 
   *yp = v;
 }
 
-template <int KW, int R, bool LN, int EPI, int KSPLIT>
+// T: float4 steps of 16 k per wave (a wave's k slice is 16 T wide); KW: waves per workgroup
+// (KW slices of 16 T cover the workgroup's part of K); R: column blocks of 16 per workgroup;
+// MB: row blocks of 16 (the batch, M <= 16 MB).
+template <int T, int KW, int R, int MB, bool LN, int EPI, int KSPLIT>
 __global__ __launch_bounds__(kWave* KW) void skinny_linear_kernel(const SkinnyArgs a) {
   static_assert(!LN || KSPLIT == 1, "the LayerNorm needs every k slice of a row in one workgroup");
+  constexpr int kRange = 16 * T;
+  constexpr int kRows = kSkinnyRows * MB;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int i = lane & 15;
   const int g = lane >> 4;
-  const int k_lo = (blockIdx.y * KW + wave) * kSkinnyRange;  // blockIdx.y: the K part (split launches)
+  const int k_lo = (blockIdx.y * KW + wave) * kRange;  // blockIdx.y: the K part (split launches)
   const int n_base = blockIdx.x * (16 * R);
 
   // gamma / beta first (needed first, after the X loads), staged to LDS for the whole K.
-  // K / 4 = 48 KW float4s of each: at most one per thread.
-  constexpr int kLnVec = KW * kSkinnyRange / 4;
+  // K / 4 = 4 T KW float4s of each: at most one per thread.
+  constexpr int kLnVec = KW * kRange / 4;
+  static_assert(!LN || kLnVec <= kWave * KW, "one gamma / beta float4 per thread");
   __shared__ float4 s_gamma[LN ? kLnVec : 1], s_beta[LN ? kLnVec : 1];
   float4 gm_ld = make_float4(0.f, 0.f, 0.f, 0.f), bt_ld = gm_ld;
   if constexpr (LN) {
@@ -108,27 +115,30 @@ __global__ __launch_bounds__(kWave* KW) void skinny_linear_kernel(const SkinnyAr
     bt_ld = reinterpret_cast<const float4*>(a.beta)[j];
   }
 
-  // This lane's slice of X: row i, k = k_lo + 16 t + 4 g + 0..3.
-  float4 xr[kSkinnyT];
-  if (i < a.M) {
-    const float* xp = a.x + (int64_t)i * a.x_stride + k_lo + 4 * g;
+  // This lane's slice of X for each row block mb: row 16 mb + i, k = k_lo + 16 t + 4 g + 0..3.
+  float4 xr[MB][T];
 #pragma unroll
-    for (int t = 0; t < kSkinnyT; ++t) xr[t] = *reinterpret_cast<const float4*>(xp + 16 * t);
-  } else {  // rows past the batch are zero
+  for (int mb = 0; mb < MB; ++mb) {
+    const int row = kSkinnyRows * mb + i;
+    if (row < a.M) {
+      const float* xp = a.x + (int64_t)row * a.x_stride + k_lo + 4 * g;
 #pragma unroll
-    for (int t = 0; t < kSkinnyT; ++t) xr[t] = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int t = 0; t < T; ++t) xr[mb][t] = *reinterpret_cast<const float4*>(xp + 16 * t);
+    } else {  // rows past the batch are zero
+#pragma unroll
+      for (int t = 0; t < T; ++t) xr[mb][t] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
   }
 
   // W rows n_base + 16 r + i; rows past N (the ragged last block) read row N - 1 and are not
   // stored.
-  auto load_w = [&](floatx4 (&wv)[kSkinnyT], int r) {
+  auto load_w = [&](floatx4 (&wv)[T], int r) {
     const int n = min(n_base + 16 * r + i, a.N - 1);
     const float* wp = a.w + (int64_t)n * a.K + k_lo + 4 * g;
 #pragma unroll
-    for (int t = 0; t < kSkinnyT; ++t)
-      wv[t] = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(wp + 16 * t));
+    for (int t = 0; t < T; ++t) wv[t] = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(wp + 16 * t));
   };
-  floatx4 wb[R > 1 ? 2 : 1][kSkinnyT];
+  floatx4 wb[R > 1 ? 2 : 1][T];
   load_w(wb[0], 0);
   if constexpr (R > 1) load_w(wb[1], 1);  // two column blocks in flight from the start
   __builtin_amdgcn_sched_barrier(0);       // keep the loads ahead of everything below
@@ -138,57 +148,74 @@ __global__ __launch_bounds__(kWave* KW) void skinny_linear_kernel(const SkinnyAr
       s_gamma[threadIdx.x] = gm_ld;
       s_beta[threadIdx.x] = bt_ld;
     }
-    // Row i's sum over this wave's slice lives in lanes i, i + 16, i + 32, i + 48.
-    __shared__ float red[2][KW][kSkinnyRows];
-    float sum = 0.f;
+    // Row 16 mb + i's sum over this wave's slice lives in lanes i, i + 16, i + 32, i + 48.
+    __shared__ float red[2][KW][kRows];
 #pragma unroll
-    for (int t = 0; t < kSkinnyT; ++t) sum += (xr[t].x + xr[t].y) + (xr[t].z + xr[t].w);
-    sum += __shfl_xor(sum, 16);
-    sum += __shfl_xor(sum, 32);
-    if (g == 0) red[0][wave][i] = sum;
-    __syncthreads();
-    float tot = 0.f;
+    for (int mb = 0; mb < MB; ++mb) {
+      float sum = 0.f;
 #pragma unroll
-    for (int w = 0; w < KW; ++w) tot += red[0][w][i];
-    const float inv_k = 1.f / (float)a.K;
-    const float mean = tot * inv_k;
-    float q = 0.f;
-#pragma unroll
-    for (int t = 0; t < kSkinnyT; ++t) {
-      const float dx = xr[t].x - mean, dy = xr[t].y - mean, dz = xr[t].z - mean, dw = xr[t].w - mean;
-      q += (dx * dx + dy * dy) + (dz * dz + dw * dw);
+      for (int t = 0; t < T; ++t) sum += (xr[mb][t].x + xr[mb][t].y) + (xr[mb][t].z + xr[mb][t].w);
+      sum += __shfl_xor(sum, 16);
+      sum += __shfl_xor(sum, 32);
+      if (g == 0) red[0][wave][kSkinnyRows * mb + i] = sum;
     }
-    q += __shfl_xor(q, 16);
-    q += __shfl_xor(q, 32);
-    if (g == 0) red[1][wave][i] = q;
     __syncthreads();
-    tot = 0.f;
+    const float inv_k = 1.f / (float)a.K;
+    float mean[MB];
 #pragma unroll
-    for (int w = 0; w < KW; ++w) tot += red[1][w][i];
-    const float rstd = rsqrtf(tot * inv_k + a.eps);
+    for (int mb = 0; mb < MB; ++mb) {
+      float tot = 0.f;
 #pragma unroll
-    for (int t = 0; t < kSkinnyT; ++t) {
-      const int j = (k_lo + 16 * t + 4 * g) / 4;
-      const float4 gm = s_gamma[j];
-      const float4 bt = s_beta[j];
-      xr[t].x = (xr[t].x - mean) * rstd * gm.x + bt.x;
-      xr[t].y = (xr[t].y - mean) * rstd * gm.y + bt.y;
-      xr[t].z = (xr[t].z - mean) * rstd * gm.z + bt.z;
-      xr[t].w = (xr[t].w - mean) * rstd * gm.w + bt.w;
+      for (int w = 0; w < KW; ++w) tot += red[0][w][kSkinnyRows * mb + i];
+      mean[mb] = tot * inv_k;
+      float q = 0.f;
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const float dx = xr[mb][t].x - mean[mb], dy = xr[mb][t].y - mean[mb];
+        const float dz = xr[mb][t].z - mean[mb], dw = xr[mb][t].w - mean[mb];
+        q += (dx * dx + dy * dy) + (dz * dz + dw * dw);
+      }
+      q += __shfl_xor(q, 16);
+      q += __shfl_xor(q, 32);
+      if (g == 0) red[1][wave][kSkinnyRows * mb + i] = q;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      float tot = 0.f;
+#pragma unroll
+      for (int w = 0; w < KW; ++w) tot += red[1][w][kSkinnyRows * mb + i];
+      const float rstd = rsqrtf(tot * inv_k + a.eps);
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const int j = (k_lo + 16 * t + 4 * g) / 4;
+        const float4 gm = s_gamma[j];
+        const float4 bt = s_beta[j];
+        xr[mb][t].x = (xr[mb][t].x - mean[mb]) * rstd * gm.x + bt.x;
+        xr[mb][t].y = (xr[mb][t].y - mean[mb]) * rstd * gm.y + bt.y;
+        xr[mb][t].z = (xr[mb][t].z - mean[mb]) * rstd * gm.z + bt.z;
+        xr[mb][t].w = (xr[mb][t].w - mean[mb]) * rstd * gm.w + bt.w;
+      }
     }
   }
 
-  floatx4 acc[R];
+  // Each W float4 feeds the MB row blocks' MFMAs (independent accumulators).
+  floatx4 acc[R][MB];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const floatx4(&wv)[kSkinnyT] = wb[r & 1];
-    acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const floatx4(&wv)[T] = wb[r & 1];
 #pragma unroll
-    for (int t = 0; t < kSkinnyT; ++t) {
-      acc[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][0], xr[t].x, acc[r], 0, 0, 0);
-      acc[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][1], xr[t].y, acc[r], 0, 0, 0);
-      acc[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][2], xr[t].z, acc[r], 0, 0, 0);
-      acc[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][3], xr[t].w, acc[r], 0, 0, 0);
+    for (int mb = 0; mb < MB; ++mb) acc[r][mb] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) acc[r][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][0], xr[mb][t].x, acc[r][mb], 0, 0, 0);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) acc[r][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][1], xr[mb][t].y, acc[r][mb], 0, 0, 0);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) acc[r][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][2], xr[mb][t].z, acc[r][mb], 0, 0, 0);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) acc[r][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][3], xr[mb][t].w, acc[r][mb], 0, 0, 0);
     }
     if (r + 2 < R) {  // block r + 2 into the registers block r just freed
       __builtin_amdgcn_sched_barrier(0);
@@ -197,28 +224,33 @@ __global__ __launch_bounds__(kWave* KW) void skinny_linear_kernel(const SkinnyAr
     }
   }
 
-  // Partial products of the KW waves: part[w][r][lane][reg], 5 floats per lane (bank spread).
-  __shared__ float part[KW][R][kWave][5];
+  // Partial products of the KW waves: part[w][r][mb][lane][reg], 5 floats per lane (bank spread).
+  __shared__ float part[KW][R][MB][kWave][5];
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) part[wave][r][lane][q] = acc[r][q];
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) part[wave][r][mb][lane][q] = acc[r][mb][q];
   __syncthreads();
 
-  // Output o = (m, nn): m = o / (16 R), column n_base + nn. Its value sits in lane m + 16 (c / 4),
-  // register c % 4 of block nn / 16, c = nn % 16.
-  constexpr int kOut = 16 * kSkinnyRows * R;
+  // Output o = (m, nn): m = o / (16 R), column n_base + nn. Its value sits in row block m / 16,
+  // lane m % 16 + 16 (c / 4), register c % 4 of column block nn / 16, c = nn % 16.
+  constexpr int kOut = 16 * R * kRows;
+  auto gather = [&](int m, int nn) {
+    const int c = nn & 15;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < KW; ++w) v += part[w][nn >> 4][m >> 4][(m & 15) + 16 * (c >> 2)][c & 3];
+    return v;
+  };
   if constexpr (KSPLIT == 1) {
     for (int o = threadIdx.x; o < kOut; o += kWave * KW) {
       const int m = o / (16 * R);
       const int nn = o - m * (16 * R);
       const int n = n_base + nn;
       if (m >= a.M || n >= a.N) continue;
-      const int c = nn & 15;
-      float v = 0.f;
-#pragma unroll
-      for (int w = 0; w < KW; ++w) v += part[w][nn >> 4][m + 16 * (c >> 2)][c & 3];
-      store_output<EPI>(a, m, n, v);
+      store_output<EPI>(a, m, n, gather(m, nn));
     }
   } else {
     float* mine = a.partials + ((int64_t)blockIdx.x * KSPLIT + blockIdx.y) * kOut;
@@ -226,11 +258,7 @@ __global__ __launch_bounds__(kWave* KW) void skinny_linear_kernel(const SkinnyAr
       const int m = o / (16 * R);
       if (m >= a.M) break;  // rows past the batch are never read
       const int nn = o - m * (16 * R);
-      const int c = nn & 15;
-      float v = 0.f;
-#pragma unroll
-      for (int w = 0; w < KW; ++w) v += part[w][nn >> 4][m + 16 * (c >> 2)][c & 3];
-      __hip_atomic_store(mine + o, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(mine + o, gather(m, nn), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
     __syncthreads();                // ... and every thread's
@@ -257,36 +285,47 @@ __global__ __launch_bounds__(kWave* KW) void skinny_linear_kernel(const SkinnyAr
   }
 }
 
-template <int KW, int R, bool LN, int KSPLIT = 1>
+template <int T, int KW, int R, int MB, bool LN, int KSPLIT>
 void launch_skinny_epi(const SkinnyArgs& a, int epi, hipStream_t s) {
   const dim3 grid((unsigned)((a.N + 16 * R - 1) / (16 * R)), KSPLIT), block(kWave * KW);
   switch (epi) {
     case kEpiGelu:
-      hipLaunchKernelGGL((skinny_linear_kernel<KW, R, LN, kEpiGelu, KSPLIT>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((skinny_linear_kernel<T, KW, R, MB, LN, kEpiGelu, KSPLIT>), grid, block, 0, s, a);
       break;
     case kEpiResidual:
-      hipLaunchKernelGGL((skinny_linear_kernel<KW, R, LN, kEpiResidual, KSPLIT>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((skinny_linear_kernel<T, KW, R, MB, LN, kEpiResidual, KSPLIT>), grid, block, 0, s, a);
       break;
-    default: hipLaunchKernelGGL((skinny_linear_kernel<KW, R, LN, kEpiBias, KSPLIT>), grid, block, 0, s, a); break;
+    default:
+      hipLaunchKernelGGL((skinny_linear_kernel<T, KW, R, MB, LN, kEpiBias, KSPLIT>), grid, block, 0, s, a);
+      break;
   }
 }
 
-// Launch shape for (N, K, LN): waves per workgroup, column blocks per workgroup, workgroups per
-// column block (K split); {0, 0, 0} when unsupported.
+// Up to two row blocks a wave keeps a 192-wide k slice of X in registers (12 float4 per row
+// block); three or four row blocks halve the slice (96 wide, twice the waves) so X, two
+// column blocks of W and the accumulators stay within the 256 VGPRs of a wave.
+template <int R, bool LN, int KSPLIT>
+void launch_skinny_rows(const SkinnyArgs& a, int epi, hipStream_t s) {
+  switch ((a.M + kSkinnyRows - 1) / kSkinnyRows) {
+    case 1: launch_skinny_epi<12, 4, R, 1, LN, KSPLIT>(a, epi, s); break;
+    case 2: launch_skinny_epi<12, 4, R, 2, LN, KSPLIT>(a, epi, s); break;
+    case 3: launch_skinny_epi<6, 8, R, 3, LN, KSPLIT>(a, epi, s); break;
+    default: launch_skinny_epi<6, 8, R, 4, LN, KSPLIT>(a, epi, s); break;
+  }
+}
+
+// Launch shape for (N, K, LN): column blocks per workgroup, workgroups per column block (K
+// split); {0, 0} when unsupported. A workgroup covers 768 of K: K = 768 in one workgroup per
+// column block (at 768 columns a split costs as much as it saves), K = 3072 (mlp.c_proj) in
+// four.
 struct SkinnyShape {
-  int kw, r, ksplit;
+  int r, ksplit;
 };
 
 SkinnyShape skinny_shape(int32_t N, int32_t K, bool ln) {
-  if (K % kSkinnyRange != 0) return {0, 0, 0};
-  const int slices = K / kSkinnyRange;
-  const int blocks = (N + 15) / 16;
-  // K = 768: one workgroup per column block (at 768 columns a split costs as much as it saves);
-  // K = 3072 (mlp.c_proj): four workgroups of four slices each per column block.
-  (void)blocks;
-  if (slices == 4) return N > 8192 ? SkinnyShape{4, 2, 1} : SkinnyShape{4, 1, 1};  // wide: the LM head
-  if (slices == 16 && !ln) return {4, 1, kSkinnyKSplit};
-  return {0, 0, 0};
+  if (K == 768) return N > 8192 ? SkinnyShape{2, 1} : SkinnyShape{1, 1};  // wide: the LM head
+  if (K == 3072 && !ln) return {1, kSkinnyKSplit};
+  return {0, 0};
 }
 
 // ------------------------------------------------------------------------------- embeddings
@@ -328,12 +367,13 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(float* x, int64_t x_str
 
 extern "C" size_t tq_skinny_linear_workspace_size(int32_t M, int32_t N, int32_t K, int32_t has_layernorm) {
   using namespace tq;
-  if (M < 1 || M > kSkinnyRows || N < 1 || K < 1) return 0;
+  if (M < 1 || M > kSkinnyRows * kSkinnyMaxBlocks || N < 1 || K < 1) return 0;
   const SkinnyShape sh = skinny_shape(N, K, has_layernorm != 0);
-  if (sh.kw == 0 || sh.ksplit == 1) return 0;
+  if (sh.r == 0 || sh.ksplit == 1) return 0;
   const int64_t blocks = (N + 16 * sh.r - 1) / (16 * sh.r);
+  const int64_t rows = (int64_t)(M + kSkinnyRows - 1) / kSkinnyRows * kSkinnyRows;
   const int64_t counters = (blocks * 4 + 255) / 256 * 256;  // arrival counters, then the partial tiles
-  return (size_t)(counters + blocks * sh.ksplit * 16 * kSkinnyRows * sh.r * 4);
+  return (size_t)(counters + blocks * sh.ksplit * 16 * sh.r * rows * 4);
 }
 
 extern "C" tq_status tq_skinny_linear(float* y, int64_t y_stride, const float* x, int64_t x_stride, int32_t M,
@@ -344,10 +384,10 @@ extern "C" tq_status tq_skinny_linear(float* y, int64_t y_stride, const float* x
   if (M < 0 || N < 1 || K < 1 || epilogue < 0 || epilogue > 2) return TQ_ERR_INVALID_ARGUMENT;
   if ((ln_gamma == nullptr) != (ln_beta == nullptr) || (ln_gamma != nullptr && !(ln_eps >= 0.f)))
     return TQ_ERR_INVALID_ARGUMENT;
-  if (M > kSkinnyRows) return TQ_ERR_UNSUPPORTED;
+  if (M > kSkinnyRows * kSkinnyMaxBlocks) return TQ_ERR_UNSUPPORTED;
   const bool ln = ln_gamma != nullptr;
   const SkinnyShape sh = skinny_shape(N, K, ln);
-  if (sh.kw == 0) return TQ_ERR_UNSUPPORTED;
+  if (sh.r == 0) return TQ_ERR_UNSUPPORTED;
   if (M == 0) return TQ_OK;
   if (y == nullptr || x == nullptr || w == nullptr) return TQ_ERR_INVALID_ARGUMENT;
   if (x_stride < K || y_stride < N) return TQ_ERR_INVALID_ARGUMENT;
@@ -378,13 +418,13 @@ extern "C" tq_status tq_skinny_linear(float* y, int64_t y_stride, const float* x
   }
   hipStream_t s = (hipStream_t)stream;
   if (sh.r == 2) {  // wide outputs
-    if (ln) launch_skinny_epi<4, 2, true>(a, epilogue, s);
-    else launch_skinny_epi<4, 2, false>(a, epilogue, s);
+    if (ln) launch_skinny_rows<2, true, 1>(a, epilogue, s);
+    else launch_skinny_rows<2, false, 1>(a, epilogue, s);
   } else if (sh.ksplit == 1) {
-    if (ln) launch_skinny_epi<4, 1, true>(a, epilogue, s);
-    else launch_skinny_epi<4, 1, false>(a, epilogue, s);
+    if (ln) launch_skinny_rows<1, true, 1>(a, epilogue, s);
+    else launch_skinny_rows<1, false, 1>(a, epilogue, s);
   } else {
-    launch_skinny_epi<4, 1, false, kSkinnyKSplit>(a, epilogue, s);
+    launch_skinny_rows<1, false, kSkinnyKSplit>(a, epilogue, s);
   }
   return check_launch();
 }

@@ -101,14 +101,15 @@ class GPT2(nn.Module):
         return h
 
     def skinny_ok(self, rows: int) -> bool:
-        """Whether a batch of ``rows`` can run through :meth:`skinny_logits` (at most 16 rows; the
-        linears' input widths n_embd and 4 * n_embd must be ones ``tq_skinny_linear`` takes)."""
+        """Whether a batch of ``rows`` can run through :meth:`skinny_logits` (at most
+        ``ops.SKINNY_MAX_ROWS`` rows; the linears' input widths n_embd and 4 * n_embd must be ones
+        ``tq_skinny_linear`` takes)."""
         C = self.cfg.n_embd
         return ops.skinny_supported(rows, C) and ops.skinny_supported(rows, 4 * C)
 
     def skinny_logits(self, x: torch.Tensor, cache) -> torch.Tensor:
-        """Logits ``[M, vocab]`` of ``M <= 16`` rows from their embeddings ``x`` ``[M, C]``, which become
-        the residual stream (updated in place). The reference's loop (tokquay/model.py:172-181) as five
+        """Logits ``[M, vocab]`` of ``M <= ops.SKINNY_MAX_ROWS`` rows from their embeddings ``x``
+        ``[M, C]``, which become the residual stream (updated in place). The reference's loop (tokquay/model.py:172-181) as five
         launches per block: ``c_attn`` with ``ln_1`` in front, attention, ``c_proj`` adding into x,
         ``c_fc`` with ``ln_2`` in front and the GELU after, ``mlp.c_proj`` adding into x; then the tied
         LM head with ``ln_f`` in front (``tq_skinny_linear``)."""

@@ -244,7 +244,11 @@ def add_layernorm(x: torch.Tensor, y: torch.Tensor, weight: torch.Tensor, bias: 
     return x_out, h
 
 
-SKINNY_MAX_ROWS = 16
+# tq_skinny_linear takes up to 64 rows; decode steps use it up to 32. Measured decode steps
+# (graphs + pipelining, contexts ~300-500): 24 / 32 sequences 0.95 / 0.98 -> 0.76 / 0.79 ms with
+# it, while at 48 / 64 (four row blocks per workgroup) hipBLASLt's GEMMs plus separate LayerNorm
+# launches were faster (1.06 / 1.11 against 1.15 / 1.20 ms).
+SKINNY_MAX_ROWS = 32
 SKINNY_WIDTHS = (768, 3072)
 _EPILOGUES = {"none": 0, "gelu": 1, "residual": 2}
 
@@ -270,14 +274,15 @@ def zeroed_scratch(device: torch.device, use: str, nbytes: int) -> torch.Tensor 
 
 
 def skinny_supported(rows: int, in_features: int) -> bool:
-    """Whether ``tq_skinny_linear`` takes this shape (at most 16 rows, K = 768 or 3072)."""
+    """Whether decode steps run this shape through ``tq_skinny_linear`` (at most ``SKINNY_MAX_ROWS``
+    rows, K = 768 or 3072)."""
     return 0 < rows <= SKINNY_MAX_ROWS and in_features in SKINNY_WIDTHS
 
 
 def skinny_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
                   ln: tuple[torch.Tensor, torch.Tensor, float] | None = None, epilogue: str = "none",
                   out: torch.Tensor | None = None) -> torch.Tensor:
-    """``epilogue(LN(x) @ weight.T + bias)`` for at most 16 float32 rows in one launch (``tq_skinny_linear``).
+    """``epilogue(LN(x) @ weight.T + bias)`` for at most 64 float32 rows in one launch (``tq_skinny_linear``).
 
     ``ln = (gamma, beta, eps)`` fuses the LayerNorm in front (tokquay/model.py:117-118); ``epilogue`` is
     ``"none"``, ``"gelu"`` (tanh form, :107) or ``"residual"``: ``out += x @ weight.T + bias`` in place (the
