@@ -252,11 +252,12 @@ tq_status tq_add_layernorm(float* x_out, int64_t x_out_stride, float* h_out, int
  * order (repeated calls give the same bits).
  *
  * Some shapes (K = 3072 with few columns) split K over several workgroups and need a
- * workspace of tq_skinny_linear_workspace_size() bytes (0: none), 256-byte
- * aligned, zeroed once before its first use: each call leaves it ready for the
- * next. Calls that share a workspace must not run concurrently.
+ * workspace of tq_skinny_linear_workspace_size() bytes (0: none; it grows with M),
+ * 256-byte aligned, zeroed once before its first use: each call leaves it ready for
+ * the next call with the same N and K (any M). Use one workspace per (N, K); calls
+ * that share a workspace must not run concurrently.
  *
- * Replaces, for decode steps of up to 32 sequences (the kernel takes 64), the c_attn / c_proj / c_fc
+ * Replaces, for decode steps of at most 64 sequences, the c_attn / c_proj / c_fc
  * / mlp.c_proj linears (tokquay/model.py:62-63, :103-104) with ln_1 / ln_2 in
  * front (:117-118), the GELU (:107) and the residual adds (:122-123), and the
  * LM head with ln_f (:180-181, W = wte, no bias).

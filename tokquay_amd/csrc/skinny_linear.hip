@@ -11,18 +11,19 @@
 //
 // Y^T[n][m] = sum_k W[n][k] X[m][k] on v_mfma_f32_16x16x4_f32: the A operand is 16
 // rows of W, the B operand X^T, so one MFMA block covers a row block of 16 batch rows
-// (rows past M are zero); up to four row blocks share each W register. Lane (i, g) =
+// (rows past M are zero); the two row blocks of a row group share each W register. Lane (i, g) =
 // (lane % 16, lane / 16) loads W[n0 + i][k .. k + 3] and X[16 mb + i][k .. k + 3] with
 // k = kb + 4 g as float4s; step j = 0..3 of the block then takes component j, so lane
 // group g supplies k = kb + 4 g + j to both operands. The accumulator's lane (j, g)
 // holds Y^T[n0 + 4 g + r][m = 16 mb + j], r = 0..3.
 //
-// Work split: a wave owns one k slice (each lane keeps its part of X in registers:
-// 12 float4 per row block for 192-wide slices at up to 32 rows, 6 for 96-wide slices
-// at up to 64) of 16 R output columns; a workgroup's waves cover 768 of K, and their
-// partial products are summed through LDS in a fixed order. Every load of W is issued
-// before anything waits: the first two column blocks at the start, block r + 2 as
-// soon as block r's products have freed its registers.
+// Work split: a wave owns one 192-wide k slice (each lane keeps its part of X in 12
+// float4 registers per row block) of 16 R output columns; a workgroup's four waves
+// cover 768 of K, and their partial products are summed through LDS in a fixed order.
+// Up to 16 rows are one row block; 17-64 rows run as row groups of two blocks, one
+// workgroup per (row group, column block). Every load of W is issued before anything
+// waits: the first two column blocks at the start, block r + 2 as soon as block r's
+// products have freed its registers.
 //
 // mlp.c_proj (768 columns, K = 3072) has 48 column blocks, too few for 256 CUs, so
 // its K is split over KSPLIT workgroups per block. Each stores its partial tile with
@@ -102,6 +103,9 @@ __global__ __launch_bounds__(kWave* KW) void skinny_linear_kernel(const SkinnyAr
   const int g = lane >> 4;
   const int k_lo = (blockIdx.y * KW + wave) * kRange;  // blockIdx.y: the K part (split launches)
   const int n_base = blockIdx.x * (16 * R);
+  const int row0 = blockIdx.z * kRows;              // blockIdx.z: the row group (more than kRows rows)
+  const int M = min(a.M - row0, kRows);             // rows of this workgroup
+  const int cb = blockIdx.z * gridDim.x + blockIdx.x;  // (row group, column block): its split workspace
 
   // gamma / beta first (needed first, after the X loads), staged to LDS for the whole K.
   // K / 4 = 4 T KW float4s of each: at most one per thread.
@@ -120,8 +124,8 @@ __global__ __launch_bounds__(kWave* KW) void skinny_linear_kernel(const SkinnyAr
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int row = kSkinnyRows * mb + i;
-    if (row < a.M) {
-      const float* xp = a.x + (int64_t)row * a.x_stride + k_lo + 4 * g;
+    if (row < M) {
+      const float* xp = a.x + (int64_t)(row0 + row) * a.x_stride + k_lo + 4 * g;
 #pragma unroll
       for (int t = 0; t < T; ++t) xr[mb][t] = *reinterpret_cast<const float4*>(xp + 16 * t);
     } else {  // rows past the batch are zero
@@ -249,14 +253,14 @@ __global__ __launch_bounds__(kWave* KW) void skinny_linear_kernel(const SkinnyAr
       const int m = o / (16 * R);
       const int nn = o - m * (16 * R);
       const int n = n_base + nn;
-      if (m >= a.M || n >= a.N) continue;
-      store_output<EPI>(a, m, n, gather(m, nn));
+      if (m >= M || n >= a.N) continue;
+      store_output<EPI>(a, row0 + m, n, gather(m, nn));
     }
   } else {
-    float* mine = a.partials + ((int64_t)blockIdx.x * KSPLIT + blockIdx.y) * kOut;
+    float* mine = a.partials + ((int64_t)cb * KSPLIT + blockIdx.y) * kOut;
     for (int o = threadIdx.x; o < kOut; o += kWave * KW) {
       const int m = o / (16 * R);
-      if (m >= a.M) break;  // rows past the batch are never read
+      if (m >= M) break;  // rows past the batch are never read
       const int nn = o - m * (16 * R);
       __hip_atomic_store(mine + o, gather(m, nn), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -264,14 +268,14 @@ __global__ __launch_bounds__(kWave* KW) void skinny_linear_kernel(const SkinnyAr
     __syncthreads();                // ... and every thread's
     __shared__ int s_last;
     if (threadIdx.x == 0)
-      s_last = __hip_atomic_fetch_add(a.arrivals + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+      s_last = __hip_atomic_fetch_add(a.arrivals + cb, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                KSPLIT - 1;
     __syncthreads();
     if (!s_last) return;
-    const float* tiles = a.partials + (int64_t)blockIdx.x * KSPLIT * kOut;
+    const float* tiles = a.partials + (int64_t)cb * KSPLIT * kOut;
     for (int o = threadIdx.x; o < kOut; o += kWave * KW) {
       const int m = o / (16 * R);
-      if (m >= a.M) break;
+      if (m >= M) break;
       const int nn = o - m * (16 * R);
       const int n = n_base + nn;
       if (n >= a.N) continue;
@@ -279,15 +283,17 @@ __global__ __launch_bounds__(kWave* KW) void skinny_linear_kernel(const SkinnyAr
 #pragma unroll
       for (int ks = 0; ks < KSPLIT; ++ks)
         v += __hip_atomic_load(tiles + ks * kOut + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      store_output<EPI>(a, m, n, v);
+      store_output<EPI>(a, row0 + m, n, v);
     }
-    if (threadIdx.x == 0) __hip_atomic_store(a.arrivals + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) __hip_atomic_store(a.arrivals + cb, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
 template <int T, int KW, int R, int MB, bool LN, int KSPLIT>
 void launch_skinny_epi(const SkinnyArgs& a, int epi, hipStream_t s) {
-  const dim3 grid((unsigned)((a.N + 16 * R - 1) / (16 * R)), KSPLIT), block(kWave * KW);
+  constexpr int kRows = kSkinnyRows * MB;
+  const dim3 grid((unsigned)((a.N + 16 * R - 1) / (16 * R)), KSPLIT, (unsigned)((a.M + kRows - 1) / kRows));
+  const dim3 block(kWave * KW);
   switch (epi) {
     case kEpiGelu:
       hipLaunchKernelGGL((skinny_linear_kernel<T, KW, R, MB, LN, kEpiGelu, KSPLIT>), grid, block, 0, s, a);
@@ -301,17 +307,15 @@ void launch_skinny_epi(const SkinnyArgs& a, int epi, hipStream_t s) {
   }
 }
 
-// Up to two row blocks a wave keeps a 192-wide k slice of X in registers (12 float4 per row
-// block); three or four row blocks halve the slice (96 wide, twice the waves) so X, two
-// column blocks of W and the accumulators stay within the 256 VGPRs of a wave.
+// A wave keeps a 192-wide k slice of X in registers: 12 float4 per row block. Up to 16 rows run
+// as one row block; more as row groups of two blocks (32 rows), one workgroup per (row group,
+// column block), each reading its columns of W (the second read of a column mostly hits the
+// memory-side cache). Four row blocks in one workgroup (96-wide slices, eight waves) left 112
+// of the 256 CUs idle at 2,304 columns and lost to this.
 template <int R, bool LN, int KSPLIT>
 void launch_skinny_rows(const SkinnyArgs& a, int epi, hipStream_t s) {
-  switch ((a.M + kSkinnyRows - 1) / kSkinnyRows) {
-    case 1: launch_skinny_epi<12, 4, R, 1, LN, KSPLIT>(a, epi, s); break;
-    case 2: launch_skinny_epi<12, 4, R, 2, LN, KSPLIT>(a, epi, s); break;
-    case 3: launch_skinny_epi<6, 8, R, 3, LN, KSPLIT>(a, epi, s); break;
-    default: launch_skinny_epi<6, 8, R, 4, LN, KSPLIT>(a, epi, s); break;
-  }
+  if (a.M <= kSkinnyRows) launch_skinny_epi<12, 4, R, 1, LN, KSPLIT>(a, epi, s);
+  else launch_skinny_epi<12, 4, R, 2, LN, KSPLIT>(a, epi, s);
 }
 
 // Launch shape for (N, K, LN): column blocks per workgroup, workgroups per column block (K
@@ -365,15 +369,28 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(float* x, int64_t x_str
 }  // namespace
 }  // namespace tq
 
+// Row groups of the launch: one of up to 16 rows, else groups of 32 (two row blocks).
+static int skinny_row_groups(int32_t M) {
+  return M <= tq::kSkinnyRows ? 1 : (M + 2 * tq::kSkinnyRows - 1) / (2 * tq::kSkinnyRows);
+}
+static int skinny_group_rows(int32_t M) { return M <= tq::kSkinnyRows ? tq::kSkinnyRows : 2 * tq::kSkinnyRows; }
+
+// Bytes of the arrival counters at the front of a split launch's workspace: room for the most
+// row groups, so that for one (N, K) the counters sit at the same place whatever M is (the
+// partial tiles behind them are left with data; a counter must never land on them).
+static int64_t skinny_counter_bytes(int64_t col_blocks) {
+  const int64_t max_groups = tq::kSkinnyMaxBlocks / 2;
+  return (col_blocks * max_groups * 4 + 255) / 256 * 256;
+}
+
 extern "C" size_t tq_skinny_linear_workspace_size(int32_t M, int32_t N, int32_t K, int32_t has_layernorm) {
   using namespace tq;
   if (M < 1 || M > kSkinnyRows * kSkinnyMaxBlocks || N < 1 || K < 1) return 0;
   const SkinnyShape sh = skinny_shape(N, K, has_layernorm != 0);
   if (sh.r == 0 || sh.ksplit == 1) return 0;
-  const int64_t blocks = (N + 16 * sh.r - 1) / (16 * sh.r);
-  const int64_t rows = (int64_t)(M + kSkinnyRows - 1) / kSkinnyRows * kSkinnyRows;
-  const int64_t counters = (blocks * 4 + 255) / 256 * 256;  // arrival counters, then the partial tiles
-  return (size_t)(counters + blocks * sh.ksplit * 16 * sh.r * rows * 4);
+  const int64_t col_blocks = (N + 16 * sh.r - 1) / (16 * sh.r);
+  const int64_t blocks = col_blocks * skinny_row_groups(M);
+  return (size_t)(skinny_counter_bytes(col_blocks) + blocks * sh.ksplit * 16 * sh.r * skinny_group_rows(M) * 4);
 }
 
 extern "C" tq_status tq_skinny_linear(float* y, int64_t y_stride, const float* x, int64_t x_stride, int32_t M,
@@ -412,9 +429,9 @@ extern "C" tq_status tq_skinny_linear(float* y, int64_t y_stride, const float* x
     const size_t need = tq_skinny_linear_workspace_size(M, N, K, ln ? 1 : 0);
     if (workspace == nullptr || workspace_bytes < need || (uintptr_t)workspace % 256 != 0)
       return TQ_ERR_WORKSPACE;
-    const int64_t blocks = (N + 16 * sh.r - 1) / (16 * sh.r);
+    const int64_t col_blocks = (N + 16 * sh.r - 1) / (16 * sh.r);
     a.arrivals = static_cast<int32_t*>(workspace);
-    a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + (blocks * 4 + 255) / 256 * 256);
+    a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + skinny_counter_bytes(col_blocks));
   }
   hipStream_t s = (hipStream_t)stream;
   if (sh.r == 2) {  // wide outputs

@@ -4,7 +4,7 @@ A decode step (every sequence feeds one token) runs ~120-180 small launches
 from Python; at 256 sequences that host work is a third of the step. This module
 captures the whole decode forward (embeddings, 12 layers with the paged-decode
 kernel that also writes the new K/V, LM head, greedy argmax) once per batch
-bucket (powers of two) into a HIP graph and replays it. Buckets of at most 32
+bucket (powers of two) into a HIP graph and replays it. Buckets of at most 64
 rows run the fused small-batch path (``GPT2.skinny_logits``: each linear with
 its LayerNorm / GELU / residual add in one ``tq_skinny_linear`` launch, about 65
 launches per step); larger buckets the library GEMMs with ``tq_add_layernorm``.
@@ -132,7 +132,7 @@ class DecodeGraphs:
     """Captured decode forwards, one per batch bucket, sharing one StaticDecodeBatch."""
 
     def __init__(self, model, allocator: BlockAllocator, max_batch: int, skinny: bool = True):
-        """``skinny``: buckets of at most 32 rows run the fused small-batch linears
+        """``skinny``: buckets of at most 64 rows run the fused small-batch linears
         (``GPT2.skinny_logits``) instead of the library GEMMs."""
         self.model = model
         self.skinny = skinny
@@ -147,7 +147,7 @@ class DecodeGraphs:
         m, s = self.model, self.static
         view = s.view(rows)
         if self.skinny and m.skinny_ok(rows):
-            # Up to 32 rows: embeddings (source rows resolved on the device) and five launches per
+            # Up to 64 rows: embeddings (source rows resolved on the device) and five launches per
             # layer, each linear with its LayerNorm / GELU / residual add fused in.
             x = ops.embed_rows(s.ids[:rows], s.positions[:rows], m.wte.weight, m.wpe.weight, src=s.src[:rows],
                                tokens=s.tokens, error_word=s.error_word)  # fmt: skip

@@ -244,11 +244,10 @@ def add_layernorm(x: torch.Tensor, y: torch.Tensor, weight: torch.Tensor, bias: 
     return x_out, h
 
 
-# tq_skinny_linear takes up to 64 rows; decode steps use it up to 32. Measured decode steps
-# (graphs + pipelining, contexts ~300-500): 24 / 32 sequences 0.95 / 0.98 -> 0.76 / 0.79 ms with
-# it, while at 48 / 64 (four row blocks per workgroup) hipBLASLt's GEMMs plus separate LayerNorm
-# launches were faster (1.06 / 1.11 against 1.15 / 1.20 ms).
-SKINNY_MAX_ROWS = 32
+# Decode steps run their linears through tq_skinny_linear up to 64 rows. Measured decode steps
+# (graphs + pipelining, contexts ~300-500): 24 / 32 / 48 / 64 sequences 0.95 / 0.98 / 1.13 / 1.18 ms
+# on hipBLASLt with separate LayerNorm launches, 0.77 / 0.80 / 1.10 / 1.14 ms with it.
+SKINNY_MAX_ROWS = 64
 SKINNY_WIDTHS = (768, 3072)
 _EPILOGUES = {"none": 0, "gelu": 1, "residual": 2}
 
