@@ -124,7 +124,9 @@ tq_status tq_cache_write(float* pool, int64_t num_blocks, int32_t num_layers, in
  * The kernel splits each sequence into partitions of partition_tokens
  * positions (a multiple of 16, at most 1024; 0 = choose automatically) and merges them with
  * a log-sum-exp pass when a sequence spans several. The merge needs
- * tq_paged_decode_workspace_size(...) bytes of device workspace.
+ * tq_paged_decode_workspace_size(...) bytes of device workspace. With 0, a launch
+ * with too few (sequence, head) pairs to fill the GPU runs one workgroup of several
+ * waves per pair instead, merged on chip: no workspace (the size function says 0).
  *
  * Replaces PagedBatch.gather (tokquay/kv_cache.py:234-242), the mask it is used
  * with (tokquay/kv_cache.py:208-214) and the attention math of

@@ -89,8 +89,14 @@ def test_decode_workspace_size(lib):
     assert lib.tq_paged_decode_workspace_size(256, 12, 64, 1024, 256) == 256 * 12 * 4 * 68 * 4
     # Automatic: 3072 (sequence, head) pairs already fill the GPU, so one 1024-position partition each.
     assert lib.tq_paged_decode_workspace_size(256, 12, 64, 1024, 0) == 0
-    assert lib.tq_paged_decode_workspace_size(64, 12, 64, 512, 0) == 64 * 12 * 4 * 68 * 4  # 128-position partitions
-    assert lib.tq_paged_decode_workspace_size(4, 12, 64, 1024, 0) == 4 * 12 * 32 * 68 * 4  # small batch: 32
+    # Automatic, small batches: one workgroup of several waves per (sequence, head), merged in LDS.
+    assert lib.tq_paged_decode_workspace_size(64, 12, 64, 512, 0) == 0
+    assert lib.tq_paged_decode_workspace_size(4, 12, 64, 1024, 0) == 0
+    # Explicit partition sizes keep the partition grid and its partials.
+    assert lib.tq_paged_decode_workspace_size(64, 12, 64, 512, 128) == 64 * 12 * 4 * 68 * 4
+    assert lib.tq_paged_decode_workspace_size(4, 12, 64, 1024, 32) == 4 * 12 * 32 * 68 * 4
+    # Beyond 16 waves x 1024 positions the automatic choice falls back to the partition grid.
+    assert lib.tq_paged_decode_workspace_size(1, 12, 64, 32768, 0) == 1 * 12 * 256 * 68 * 4  # 128-position
     assert lib.tq_paged_decode_workspace_size(4, 12, 64, 1024, 20) == 0  # invalid partition
     assert lib.tq_paged_decode_workspace_size(4, 12, 64, 4096, 2048) == 0  # partitions are at most 1024
 

@@ -130,22 +130,26 @@ def test_decode_dispatch_order_does_not_change_results():
         i += cdiv(c, 16)
     tables, cl = tables.cuda(), torch.tensor(ctx, dtype=torch.int32, device="cuda")
     q = torch.randn(len(ctx), 768, generator=torch.Generator().manual_seed(14)).cuda()
-    outs = []
-    for order in (None, sorted(range(len(ctx)), key=lambda b: -ctx[b]), torch.randperm(len(ctx)).tolist()):
-        out = torch.empty_like(q)
-        so = None if order is None else torch.tensor(order, dtype=torch.int32, device="cuda")
-        ops.paged_decode(out, q, pool, 0, tables, cl, max(ctx), partition_tokens=64, seq_order=so)
-        outs.append(out)
-    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
-    err = torch.zeros(1, dtype=torch.int32, device="cuda")
-    bad = torch.arange(len(ctx), dtype=torch.int32, device="cuda")
-    bad[3] = len(ctx) + 7
-    out = torch.zeros_like(q)
-    ops.paged_decode(out, q, pool, 0, tables, cl, max(ctx), seq_order=bad, d_error=err)
-    torch.cuda.synchronize()
-    assert int(err.item()) == _lib.DEVERR_ORDER
-    keep = [b for b in range(len(ctx)) if b != 3]
-    assert torch.equal(out[keep], outs[0][keep])
+    # 64-position partitions (partition grid + merge) and the automatic choice, which at 40 sequences
+    # is the small-batch kernel (one workgroup of several waves per (sequence, head)).
+    for partition_tokens in (64, 0):
+        outs = []
+        for order in (None, sorted(range(len(ctx)), key=lambda b: -ctx[b]), torch.randperm(len(ctx)).tolist()):
+            out = torch.empty_like(q)
+            so = None if order is None else torch.tensor(order, dtype=torch.int32, device="cuda")
+            ops.paged_decode(out, q, pool, 0, tables, cl, max(ctx), partition_tokens=partition_tokens, seq_order=so)
+            outs.append(out)
+        assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+        err = torch.zeros(1, dtype=torch.int32, device="cuda")
+        bad = torch.arange(len(ctx), dtype=torch.int32, device="cuda")
+        bad[3] = len(ctx) + 7
+        out = torch.zeros_like(q)
+        ops.paged_decode(out, q, pool, 0, tables, cl, max(ctx), partition_tokens=partition_tokens, seq_order=bad,
+                         d_error=err)  # fmt: skip
+        torch.cuda.synchronize()
+        assert int(err.item()) == _lib.DEVERR_ORDER
+        keep = [b for b in range(len(ctx)) if b != 3]
+        assert torch.equal(out[keep], outs[0][keep])
 
 
 def test_decode_config4_scale():

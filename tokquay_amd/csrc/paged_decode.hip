@@ -77,6 +77,7 @@ struct DecodeArgs {
   int32_t ctx_cap;  // min(max_blocks * block_size, max_parts * part_tokens)
   int32_t part_tokens;
   int32_t max_parts;
+  int32_t split_waves;  // > 0: the small-batch kernel with this many waves per (sequence, head)
 };
 
 __device__ __forceinline__ int load_context(const DecodeArgs& a, int b, bool report) {
@@ -257,49 +258,15 @@ __device__ __forceinline__ void consume_chunk(const float4 q4, const float4 (&kx
   }
 }
 
+// One wave's pass over positions [t_begin, t_end) of sequence b, head h (t_begin < t_end <=
+// ctx): online softmax per DPP row, the four rows merged at the end, so every lane leaves with
+// (m, l) and lane r * 16 + i with acc = dims 4 i .. 4 i + 3 (the same in each row r). In the
+// write variant a wave whose range holds the new position ctx - 1 reads it from the projection
+// output and stores it into the pool after its last read.
 template <int BS_CT, bool WRITE>
-__global__ __launch_bounds__(kWave* kHeadsPerGroup) void decode_partition_kernel(const DecodeArgs a) {
-  const int lane = threadIdx.x & (kWave - 1);
-  // Workgroup p runs on XCD p % 8 and each XCD deals its workgroups to its 32 CUs round
-  // robin, so dispatches 256 s .. 256 s + 255 put one workgroup on every CU. With the
-  // longest contexts listed first, reversing every other such stratum gives each CU
-  // long and short items in turn instead of the longest of every stratum to the same
-  // CUs (measured at 256 sequences, contexts U[256,1024]: 153 -> 151 us per launch).
-  int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
-  {
-    const int gx = gridDim.x, gy = gridDim.y;
-    const int total = gx * gy * (int)gridDim.z;
-    int idx = bx + gx * (by + gy * bz);
-    const int s = idx / kCuStratum;
-    if (s & 1) idx = s * kCuStratum + min(kCuStratum, total - s * kCuStratum) - 1 - (idx - s * kCuStratum);
-    bx = idx % gx;
-    by = (idx / gx) % gy;
-    bz = idx / (gx * gy);
-  }
-  const int h = bx * kHeadsPerGroup + (threadIdx.x / kWave);
-  const int part = by;
-  if (h >= a.num_heads) return;  // whole wave leaves; the kernel has no barriers
-  // Workgroups are dispatched in grid order and older waves win arbitration, so a caller
-  // that lists the longest contexts first shortens the tail of the launch.
-  int b = bz;
-  if (a.seq_order != nullptr) {
-    b = a.seq_order[bz];
-    if ((uint32_t)b >= (uint32_t)a.num_seqs) {
-      if (h == 0 && part == 0 && lane == 0) flag_error(a.d_error, TQ_DEVERR_ORDER);
-      return;
-    }
-  }
+__device__ __forceinline__ void attend_range(const DecodeArgs& a, int b, int h, int ctx, int t_begin, int t_end,
+                                             int lane, float& m, float& l, float4& acc) {
   const int bs = BS_CT > 0 ? BS_CT : a.block_size;
-  const int ctx = load_context(a, b, part == 0 && h == 0 && lane == 0);
-  float* out_row = a.out + (int64_t)b * a.out_stride + h * kHeadDim;
-  if (ctx == 0) {
-    if (part == 0) out_row[lane] = 0.f;
-    return;
-  }
-  const int t_begin = part * a.part_tokens;
-  if (t_begin >= ctx) return;
-  const int t_end = min(ctx, t_begin + a.part_tokens);
-
   const int r = lane >> 4;        // DPP row: owns positions t0 + 4j + r
   const int c = (lane & 15) * 4;  // dims c .. c+3
   const float4 qraw =
@@ -308,9 +275,9 @@ __global__ __launch_bounds__(kWave* kHeadsPerGroup) void decode_partition_kernel
   const int32_t* bt = a.block_tables + (int64_t)b * a.bt_stride;
   const float* head_base = a.pool_layer + (int64_t)h * a.head_stride + c;
 
-  float m = -INFINITY;
-  float l = 0.f;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  m = -INFINITY;
+  l = 0.f;
+  acc = make_float4(0.f, 0.f, 0.f, 0.f);
 
   PartitionBlocks pb{0, 0, 0};
   if constexpr (BS_CT >= kChunk) pb = load_partition_blocks<BS_CT>(a, bt, t_begin, t_end, lane);
@@ -369,6 +336,56 @@ __global__ __launch_bounds__(kWave* kHeadsPerGroup) void decode_partition_kernel
     if (t_new >= 0) write_new_row<BS_CT>(a, bt, pb, bs, h, t_new, lane, c, knew, vnew);
   }
 
+}
+
+template <int BS_CT, bool WRITE>
+__global__ __launch_bounds__(kWave* kHeadsPerGroup) void decode_partition_kernel(const DecodeArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  // Workgroup p runs on XCD p % 8 and each XCD deals its workgroups to its 32 CUs round
+  // robin, so dispatches 256 s .. 256 s + 255 put one workgroup on every CU. With the
+  // longest contexts listed first, reversing every other such stratum gives each CU
+  // long and short items in turn instead of the longest of every stratum to the same
+  // CUs (measured at 256 sequences, contexts U[256,1024]: 153 -> 151 us per launch).
+  int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+  {
+    const int gx = gridDim.x, gy = gridDim.y;
+    const int total = gx * gy * (int)gridDim.z;
+    int idx = bx + gx * (by + gy * bz);
+    const int s = idx / kCuStratum;
+    if (s & 1) idx = s * kCuStratum + min(kCuStratum, total - s * kCuStratum) - 1 - (idx - s * kCuStratum);
+    bx = idx % gx;
+    by = (idx / gx) % gy;
+    bz = idx / (gx * gy);
+  }
+  const int h = bx * kHeadsPerGroup + (threadIdx.x / kWave);
+  const int part = by;
+  if (h >= a.num_heads) return;  // whole wave leaves; the kernel has no barriers
+  // Workgroups are dispatched in grid order and older waves win arbitration, so a caller
+  // that lists the longest contexts first shortens the tail of the launch.
+  int b = bz;
+  if (a.seq_order != nullptr) {
+    b = a.seq_order[bz];
+    if ((uint32_t)b >= (uint32_t)a.num_seqs) {
+      if (h == 0 && part == 0 && lane == 0) flag_error(a.d_error, TQ_DEVERR_ORDER);
+      return;
+    }
+  }
+  const int ctx = load_context(a, b, part == 0 && h == 0 && lane == 0);
+  float* out_row = a.out + (int64_t)b * a.out_stride + h * kHeadDim;
+  if (ctx == 0) {
+    if (part == 0) out_row[lane] = 0.f;
+    return;
+  }
+  const int t_begin = part * a.part_tokens;
+  if (t_begin >= ctx) return;
+  const int t_end = min(ctx, t_begin + a.part_tokens);
+
+  float m, l;
+  float4 acc;
+  attend_range<BS_CT, WRITE>(a, b, h, ctx, t_begin, t_end, lane, m, l, acc);
+  const int r = lane >> 4;
+  const int c = (lane & 15) * 4;
+
   const int nparts = (ctx + a.part_tokens - 1) / a.part_tokens;
   if (nparts == 1) {
     if (r == 0) {
@@ -382,6 +399,61 @@ __global__ __launch_bounds__(kWave* kHeadsPerGroup) void decode_partition_kernel
       pp[kHeadDim] = m;
       pp[kHeadDim + 1] = l;
     }
+  }
+}
+
+// Small batches: one workgroup of W waves per (sequence, head). Wave w takes positions
+// [w P, (w + 1) P) with P = ceil(ctx / W) rounded up to a chunk, and the W partial states
+// (m, l, acc) meet in LDS: no partials in memory and no second launch. Used where the
+// one-wave-per-partition grid would need partitions (fewer than ~3072 (sequence, head)
+// pairs), with W = the partitions it would have used (at most 16).
+template <int BS_CT, bool WRITE, int W>
+__global__ __launch_bounds__(kWave* W) void decode_split_kernel(const DecodeArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int h = blockIdx.x;
+  int b = blockIdx.y;
+  if (a.seq_order != nullptr) {
+    b = a.seq_order[blockIdx.y];
+    if ((uint32_t)b >= (uint32_t)a.num_seqs) {  // uniform across the workgroup
+      if (h == 0 && threadIdx.x == 0) flag_error(a.d_error, TQ_DEVERR_ORDER);
+      return;
+    }
+  }
+  const int ctx = load_context(a, b, h == 0 && threadIdx.x == 0);
+  float* out_row = a.out + (int64_t)b * a.out_stride + h * kHeadDim;
+  if (ctx == 0) {  // uniform across the workgroup
+    if (wave == 0) out_row[lane] = 0.f;
+    return;
+  }
+  const int span = ((ctx + W - 1) / W + kChunk - 1) / kChunk * kChunk;  // <= 1024: ctx <= ctx_cap
+  const int t_begin = wave * span;
+  const int t_end = min(ctx, t_begin + span);
+  float m = -INFINITY, l = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (t_begin < t_end) attend_range<BS_CT, WRITE>(a, b, h, ctx, t_begin, t_end, lane, m, l, acc);  // uniform
+
+  __shared__ float s_acc[W][kHeadDim];
+  __shared__ float s_ml[W][2];
+  if (lane < 16) *reinterpret_cast<float4*>(&s_acc[wave][4 * lane]) = acc;
+  if (lane == 0) {
+    s_ml[wave][0] = m;
+    s_ml[wave][1] = l;
+  }
+  __syncthreads();
+  if (wave == 0) {  // lane = output dim; the waves' states in a fixed order
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < W; ++w) M = fmaxf(M, s_ml[w][0]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const float mw = s_ml[w][0];
+      const float cw = mw == -INFINITY ? 0.f : __expf(mw - M);  // waves with no positions weigh 0
+      L = fmaf(s_ml[w][1], cw, L);
+      O = fmaf(s_acc[w][lane], cw, O);
+    }
+    out_row[lane] = O / L;
   }
 }
 
@@ -453,8 +525,38 @@ int num_partitions(int32_t max_context_len, int part) {
   return max_context_len <= 0 ? 1 : (max_context_len + part - 1) / part;
 }
 
+// Waves per (sequence, head) workgroup of the small-batch kernel, or 0 for the one-wave-per-
+// partition grid: where the automatic partitioning would split sequences, the next power of two
+// of its partition count (at most 16), so the same parallelism needs no partials and no merge
+// launch (8 sequences, contexts 300-500: 12.4 -> ... us per layer). Explicit partition sizes
+// keep the partition grid.
+int split_waves(int32_t num_seqs, int32_t num_heads, int32_t max_context_len, int32_t requested) {
+  if (requested > 0 || max_context_len <= 0) return 0;
+  const int parts = num_partitions(max_context_len, choose_partition(num_seqs, num_heads, max_context_len, 0));
+  if (parts <= 1) return 0;
+  int w = 2;
+  while (w < parts && w < 16) w *= 2;
+  return (int64_t)max_context_len <= (int64_t)w * kMaxPartition ? w : 0;
+}
+
+template <int BS_CT, bool WRITE, int W>
+void launch_split(const DecodeArgs& a, int num_seqs, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+  const dim3 grid((unsigned)a.num_heads, (unsigned)num_seqs), block(kWave * W);
+  if (start == nullptr && stop == nullptr)
+    hipLaunchKernelGGL((decode_split_kernel<BS_CT, WRITE, W>), grid, block, 0, stream, a);
+  else
+    hipExtLaunchKernelGGL((decode_split_kernel<BS_CT, WRITE, W>), grid, block, 0, stream, start, stop, 0, a);
+}
+
 template <int BS_CT, bool WRITE>
 void launch_decode(const DecodeArgs& a, int num_seqs, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+  switch (a.split_waves) {
+    case 2: launch_split<BS_CT, WRITE, 2>(a, num_seqs, stream, start, stop); return;
+    case 4: launch_split<BS_CT, WRITE, 4>(a, num_seqs, stream, start, stop); return;
+    case 8: launch_split<BS_CT, WRITE, 8>(a, num_seqs, stream, start, stop); return;
+    case 16: launch_split<BS_CT, WRITE, 16>(a, num_seqs, stream, start, stop); return;
+    default: break;
+  }
   const dim3 block(kWave * kHeadsPerGroup);
   const unsigned hgroups = (unsigned)((a.num_heads + kHeadsPerGroup - 1) / kHeadsPerGroup);
   const bool merge = a.max_parts > 1;
@@ -481,6 +583,7 @@ extern "C" size_t tq_paged_decode_workspace_size(int32_t num_seqs, int32_t num_h
   using namespace tq;
   if (num_seqs <= 0 || num_heads <= 0 || head_dim != kHeadDim || max_context_len <= 0) return 0;
   if (partition_tokens < 0 || partition_tokens % kChunk != 0 || partition_tokens > kMaxPartition) return 0;
+  if (split_waves(num_seqs, num_heads, max_context_len, partition_tokens) > 0) return 0;
   const int part = choose_partition(num_seqs, num_heads, max_context_len, partition_tokens);
   const int parts = num_partitions(max_context_len, part);
   if (parts <= 1) return 0;
@@ -553,7 +656,9 @@ tq_status paged_decode_impl(float* out, int64_t out_row_stride, const float* q, 
   a.num_heads = num_heads;
   a.block_size = block_size;
   const int64_t cap_blocks = (int64_t)max_blocks_per_seq * block_size;
-  const int64_t cap_grid = (int64_t)parts * part;
+  a.split_waves = split_waves(num_seqs, num_heads, max_context_len, partition_tokens);
+  // The grid's reach: parts x part positions, or 1024 per wave of a split workgroup.
+  const int64_t cap_grid = a.split_waves > 0 ? (int64_t)a.split_waves * kMaxPartition : (int64_t)parts * part;
   a.ctx_cap = (int32_t)(cap_blocks < cap_grid ? cap_blocks : cap_grid);
   a.part_tokens = part;
   a.max_parts = parts;
