@@ -2,9 +2,9 @@
 
 * Against torch on the CPU in fp32: ``F.linear`` with ``F.layer_norm`` in front and the GELU (tanh
   form) or residual add after (tokquay/model.py:62-63, :103-107, :117-123, :180), at GPT-2's shapes
-  including the ragged LM head (50257 columns), 1 to 16 rows, strided rows.
+  including the ragged LM head (50257 columns), 1 to 64 rows, strided rows.
 * The graph-replayed decode step through the fused path against the same step through the library
-  GEMMs: logits within fp32 tolerance and identical greedy ids, across buckets 1 to 16.
+  GEMMs: logits within fp32 tolerance and identical greedy ids, across buckets 1 to 64.
 """
 
 from __future__ import annotations

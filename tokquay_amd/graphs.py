@@ -54,11 +54,13 @@ class StaticDecodeBatch:
         self.max_blocks = cdiv(n_positions, self.block_size)
         dev = pool.device
         cap, mb = capacity, self.max_blocks
-        self.d64 = torch.zeros(3 * cap, dtype=torch.int64, device=dev)  # ids | positions | source rows
-        # tables | context lengths | dispatch order (rows by decreasing context)
-        self.d32 = torch.zeros(cap * mb + 2 * cap, dtype=torch.int32, device=dev)
-        self.h64 = torch.zeros(3 * cap, dtype=torch.int64, pin_memory=True)
-        self.h32 = torch.zeros(cap * mb + 2 * cap, dtype=torch.int32, pin_memory=True)
+        # One staging buffer and one device buffer (one copy per step): int64 ids | positions |
+        # source rows, then int32 tables | context lengths | dispatch order (rows by decreasing context).
+        b64, b32 = 8 * 3 * cap, 4 * (cap * mb + 2 * cap)
+        self.dbuf = torch.zeros(b64 + b32, dtype=torch.uint8, device=dev)
+        self.hbuf = torch.zeros(b64 + b32, dtype=torch.uint8, pin_memory=True)
+        self.d64, self.d32 = self.dbuf[:b64].view(torch.int64), self.dbuf[b64:].view(torch.int32)
+        self.h64, self.h32 = self.hbuf[:b64].view(torch.int64), self.hbuf[b64:].view(torch.int32)
         self.copied = torch.cuda.Event()
         self.ids, self.positions, self.src = self.d64[:cap], self.d64[cap : 2 * cap], self.d64[2 * cap :]
         self.tokens = torch.zeros(cap, dtype=torch.int64, device=dev)  # greedy ids of the latest replay
@@ -94,8 +96,7 @@ class StaticDecodeBatch:
         # longest-first dispatch order, with the padding rows (context 0) up to the bucket.
         _lib.native().fill_decode(seqs, bucket, src_rows, self.h64.data_ptr(), self.h64.numel(), self.h32.data_ptr(),
                                   self.h32.numel(), self.capacity, self.max_blocks, self.block_size, self.max_ctx)
-        self.d64.copy_(self.h64, non_blocking=True)
-        self.d32.copy_(self.h32, non_blocking=True)
+        self.dbuf.copy_(self.hbuf, non_blocking=True)
         self.copied.record()
 
     def view(self, bucket: int) -> "StaticDecodeView":
