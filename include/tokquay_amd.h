@@ -229,7 +229,8 @@ tq_status tq_argmax_rows(int64_t* out, const float* logits, int64_t num_rows, in
  * (biased variance, as torch's LayerNorm). Row r of each matrix starts at
  * ptr + r * stride (elements). cols a multiple of 4, at most 2048; pointers and
  * strides 16-byte aligned. Outputs may alias inputs element for element
- * (x_out == x is the in-place residual update).
+ * (x_out == x is the in-place residual update). y may be NULL (y_stride is
+ * then ignored): s = x, a plain LayerNorm.
  *
  * Replaces the residual adds of Block.forward (tokquay/model.py:122-123) with
  * the LayerNorm that follows each (ln_2, the next block's ln_1, ln_f at :180).

@@ -207,6 +207,18 @@ def test_add_layernorm_matches_torch(rows, cols):
     torch.testing.assert_close(h.cpu(), h_ref, rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("rows,cols", [(256, 768), (3, 4), (9, 1028)])
+def test_layernorm_without_add(rows, cols):
+    """``y=None``: the plain LayerNorm of x, x_out == x bit for bit (also in place)."""
+    g = torch.Generator().manual_seed(rows + cols)
+    x = torch.randn(rows, cols, generator=g) * 2 - 1
+    w, b = torch.randn(cols, generator=g), torch.randn(cols, generator=g)
+    xd = x.cuda()
+    s, h = ops.add_layernorm(xd, None, w.cuda(), b.cuda(), 1e-5, x_out=xd)
+    assert s.data_ptr() == xd.data_ptr() and torch.equal(s.cpu(), x)
+    torch.testing.assert_close(h.cpu(), torch.nn.functional.layer_norm(x, (cols,), w, b, 1e-5), rtol=1e-5, atol=1e-5)
+
+
 def test_add_layernorm_in_place_and_strided_views():
     g = torch.Generator().manual_seed(3)
     big = torch.randn(16, 2 * 768, generator=g).cuda()

@@ -7,6 +7,7 @@
 // the next LayerNorm (ln_2, the next block's ln_1, or ln_f at :180), and the
 // embedding sum before the first ln_1. Fusing the add into the LayerNorm reads
 // x and y once, writes x_out and h once, and replaces two launches with one.
+// Without y (null) it is the plain LayerNorm of x: s = x.
 // Outputs may alias inputs element for element (each lane reads its elements
 // before it writes them): x_out = x is the in-place residual update.
 //
@@ -45,8 +46,12 @@ __global__ __launch_bounds__(kWave* kRowsPerGroup) void add_layernorm_kernel(
     const int c = (v * kWave + lane) * 4;
     if (c < cols) {
       const float4 a = *reinterpret_cast<const float4*>(xr + c);
-      const float4 b = *reinterpret_cast<const float4*>(yr + c);
-      s[v] = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+      if (y != nullptr) {
+        const float4 b = *reinterpret_cast<const float4*>(yr + c);
+        s[v] = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+      } else {
+        s[v] = a;
+      }
     } else {
       s[v] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
@@ -91,8 +96,9 @@ extern "C" tq_status tq_add_layernorm(float* x_out, int64_t x_out_stride, float*
   if (rows < 0 || cols < 1 || !(eps >= 0.f)) return TQ_ERR_INVALID_ARGUMENT;
   if (cols % 4 != 0 || cols > kWave * 4 * 8) return TQ_ERR_UNSUPPORTED;
   if (rows == 0) return TQ_OK;
-  if (x_out == nullptr || h_out == nullptr || x == nullptr || y == nullptr || gamma == nullptr || beta == nullptr)
+  if (x_out == nullptr || h_out == nullptr || x == nullptr || gamma == nullptr || beta == nullptr)
     return TQ_ERR_INVALID_ARGUMENT;
+  if (y == nullptr) y_stride = cols;
   if (x_out_stride < cols || h_out_stride < cols || x_stride < cols || y_stride < cols)
     return TQ_ERR_INVALID_ARGUMENT;
   if (((uintptr_t)x_out | (uintptr_t)h_out | (uintptr_t)x | (uintptr_t)y | (uintptr_t)gamma | (uintptr_t)beta) %

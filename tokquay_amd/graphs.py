@@ -147,16 +147,15 @@ class DecodeGraphs:
     def _forward(self, rows: int) -> torch.Tensor:
         m, s = self.model, self.static
         view = s.view(rows)
+        # Embeddings in one launch, source rows resolved on the device.
+        x = ops.embed_rows(s.ids[:rows], s.positions[:rows], m.wte.weight, m.wpe.weight, src=s.src[:rows],
+                           tokens=s.tokens, error_word=s.error_word)  # fmt: skip
         if self.skinny and m.skinny_ok(rows):
-            # Up to 64 rows: embeddings (source rows resolved on the device) and five launches per
-            # layer, each linear with its LayerNorm / GELU / residual add fused in.
-            x = ops.embed_rows(s.ids[:rows], s.positions[:rows], m.wte.weight, m.wpe.weight, src=s.src[:rows],
-                               tokens=s.tokens, error_word=s.error_word)  # fmt: skip
+            # Up to 64 rows: five launches per layer, each linear with its LayerNorm / GELU /
+            # residual add fused in.
             logits = m.skinny_logits(x, view)
         else:
-            src = s.src[:rows]
-            ids = torch.where(src >= 0, s.tokens.index_select(0, src.clamp(min=0)), s.ids[:rows])
-            logits = m.trunk(ids, s.positions[:rows], view) @ m.wte.weight.T
+            logits = m.trunk(None, None, view, embedded=x) @ m.wte.weight.T
         ops.argmax_rows(logits, out=s.tokens[:rows])
         return logits
 

@@ -83,16 +83,22 @@ class GPT2(nn.Module):
         self.h = nn.ModuleList(Block(self.cfg) for _ in range(self.cfg.n_layer))
         self.ln_f = nn.LayerNorm(self.cfg.n_embd, eps=self.cfg.layer_norm_eps)
 
-    def trunk(self, ids: torch.Tensor, positions: torch.Tensor, cache) -> torch.Tensor:
+    def trunk(self, ids: torch.Tensor | None, positions: torch.Tensor | None, cache,
+              embedded: torch.Tensor | None = None) -> torch.Tensor:
         """Final hidden states ``ln_f(x)`` ``[N, C]`` of packed rows (token ids and positions ``[N]``).
 
         The reference's loop (tokquay/model.py:172-180): embeddings, ``x = x + attn(ln_1(x))``,
         ``x = x + mlp(ln_2(x))`` per block, ``ln_f``. Every residual add runs fused with the
         LayerNorm that follows it (``tq_add_layernorm``); the embedding sum is fused with the
-        first ``ln_1``. ``cache`` provides ``attend(layer, qkv)``."""
+        first ``ln_1``. ``cache`` provides ``attend(layer, qkv)``. ``embedded``: the rows' embedding
+        sums ``wte[id] + wpe[pos]`` ``[N, C]`` if already computed (``ops.embed_rows``; ``ids`` and
+        ``positions`` are then unused), updated in place as the residual stream."""
         blocks = self.h
         first = blocks[0].ln_1
-        x, h = ops.add_layernorm(self.wte(ids), self.wpe(positions), first.weight, first.bias, first.eps)
+        if embedded is None:
+            x, h = ops.add_layernorm(self.wte(ids), self.wpe(positions), first.weight, first.bias, first.eps)
+        else:
+            x, h = ops.add_layernorm(embedded, None, first.weight, first.bias, first.eps, x_out=embedded)
         for i, block in enumerate(blocks):
             a = block.attn(h, cache, i)
             x, h = ops.add_layernorm(x, a, block.ln_2.weight, block.ln_2.bias, block.ln_2.eps, x_out=x)

@@ -217,15 +217,16 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.
     return out
 
 
-def add_layernorm(x: torch.Tensor, y: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float,
+def add_layernorm(x: torch.Tensor, y: torch.Tensor | None, weight: torch.Tensor, bias: torch.Tensor, eps: float,
                   x_out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """``(x + y, layer_norm(x + y))`` for float32 rows ``[R, C]`` in one pass (``tq_add_layernorm``): a
     residual add of Block.forward (tokquay/model.py:122-123) and the LayerNorm after it. ``x_out``
-    (default: a new tensor) may be ``x`` itself for an in-place residual update."""
-    if x.dim() != 2 or y.shape != x.shape or not x.is_cuda:
+    (default: a new tensor) may be ``x`` itself for an in-place residual update. ``y=None``: ``(x,
+    layer_norm(x))``."""
+    if x.dim() != 2 or (y is not None and y.shape != x.shape) or not x.is_cuda:
         raise ValueError("x and y must be [rows, cols] tensors of one shape on a HIP device")
     rows, cols = x.shape
-    for name, t in (("x", x), ("y", y)):
+    for name, t in (("x", x),) + ((("y", y),) if y is not None else ()):
         if t.dtype != torch.float32 or t.device != x.device or t.stride(1) != 1:
             raise ValueError(f"{name} must be float32 with contiguous rows on {x.device}")
     for name, t in (("weight", weight), ("bias", bias)):
@@ -238,7 +239,8 @@ def add_layernorm(x: torch.Tensor, y: torch.Tensor, weight: torch.Tensor, bias: 
     h = torch.empty(rows, cols, dtype=torch.float32, device=x.device)
     stride = lambda t: t.stride(0) if rows > 1 else cols  # noqa: E731  (a one-row view may carry any stride)
     st = _lib.lib().tq_add_layernorm(x_out.data_ptr(), stride(x_out), h.data_ptr(), cols, x.data_ptr(), stride(x),
-                                     y.data_ptr(), stride(y), weight.data_ptr(), bias.data_ptr(), rows, cols,
+                                     y.data_ptr() if y is not None else None, stride(y) if y is not None else cols,
+                                     weight.data_ptr(), bias.data_ptr(), rows, cols,
                                      float(eps), _stream(x.device))  # fmt: skip
     _lib.check(st, "tq_add_layernorm")
     return x_out, h
