@@ -14,14 +14,15 @@
 // One 64-lane wave per row; the row stays in registers (each lane holds VEC
 // float4s of a row of at most 64 * 4 * VEC columns), so the statistics are an
 // exact two-pass mean / variance over registers: a wave sum by cross-lane
-// shuffles for each. HBM bound, 4 rows per 256-thread workgroup.
+// shuffles for each. HBM bound, one row per 64-thread workgroup (at a few hundred
+// rows the launch is latency bound; single-wave groups spread over more CUs).
 
 #include "tq_internal.h"
 
 namespace tq {
 namespace {
 
-constexpr int kRowsPerGroup = 4;
+constexpr int kRowsPerGroup = 1;  // 2.75 us per launch at 256 x 768 vs 3.05 with four rows per group
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -39,12 +40,16 @@ __global__ __launch_bounds__(kWave* kRowsPerGroup) void add_layernorm_kernel(
   if (row >= rows) return;  // whole wave
   const float* xr = x + row * x_stride;
   const float* yr = y + row * y_stride;
-  float4 s[VEC];
+  // gamma and beta are read up front: the outputs are not restrict, so loads of them placed
+  // between the stores below would each wait for the store before them.
+  float4 s[VEC], g[VEC], bt[VEC];
   float sum = 0.f;
 #pragma unroll
   for (int v = 0; v < VEC; ++v) {
     const int c = (v * kWave + lane) * 4;
     if (c < cols) {
+      g[v] = *reinterpret_cast<const float4*>(gamma + c);
+      bt[v] = *reinterpret_cast<const float4*>(beta + c);
       const float4 a = *reinterpret_cast<const float4*>(xr + c);
       if (y != nullptr) {
         const float4 b = *reinterpret_cast<const float4*>(yr + c);
@@ -53,7 +58,7 @@ __global__ __launch_bounds__(kWave* kRowsPerGroup) void add_layernorm_kernel(
         s[v] = a;
       }
     } else {
-      s[v] = make_float4(0.f, 0.f, 0.f, 0.f);
+      s[v] = g[v] = bt[v] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     sum += (s[v].x + s[v].y) + (s[v].z + s[v].w);
   }
@@ -75,12 +80,10 @@ __global__ __launch_bounds__(kWave* kRowsPerGroup) void add_layernorm_kernel(
   for (int v = 0; v < VEC; ++v) {
     const int c = (v * kWave + lane) * 4;
     if (c < cols) {
-      const float4 g = *reinterpret_cast<const float4*>(gamma + c);
-      const float4 bt = *reinterpret_cast<const float4*>(beta + c);
       *reinterpret_cast<float4*>(xo + c) = s[v];
-      *reinterpret_cast<float4*>(ho + c) =
-          make_float4((s[v].x - mean) * rstd * g.x + bt.x, (s[v].y - mean) * rstd * g.y + bt.y,
-                      (s[v].z - mean) * rstd * g.z + bt.z, (s[v].w - mean) * rstd * g.w + bt.w);
+      *reinterpret_cast<float4*>(ho + c) = make_float4(
+          (s[v].x - mean) * rstd * g[v].x + bt[v].x, (s[v].y - mean) * rstd * g[v].y + bt[v].y,
+          (s[v].z - mean) * rstd * g[v].z + bt[v].z, (s[v].w - mean) * rstd * g[v].w + bt[v].w);
     }
   }
 }
