@@ -5,9 +5,10 @@ from Python; at 256 sequences that host work is a third of the step. This module
 captures the whole decode forward (embeddings, 12 layers with the paged-decode
 kernel that also writes the new K/V, LM head, greedy argmax) once per batch
 bucket (powers of two) into a HIP graph and replays it. Buckets of at most 64
-rows run the fused small-batch path (``GPT2.skinny_logits``: each linear with
-its LayerNorm / GELU / residual add in one ``tq_skinny_linear`` launch, about 65
-launches per step); larger buckets the library GEMMs with ``tq_add_layernorm``.
+rows run the fused small-batch path (``GPT2.skinny_logits``: each linear of a
+block with its LayerNorm / GELU / residual add in one ``tq_skinny_linear`` launch,
+about 65 launches per step; ``ln_f`` and the LM head on hipBLASLt); larger buckets
+the library GEMMs with ``tq_add_layernorm``.
 
 What changes between steps lives in static device buffers at fixed addresses,
 refreshed by one host-to-device copy per step: token ids, positions,

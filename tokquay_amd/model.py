@@ -117,8 +117,9 @@ class GPT2(nn.Module):
         """Logits ``[M, vocab]`` of ``M <= ops.SKINNY_MAX_ROWS`` rows from their embeddings ``x``
         ``[M, C]``, which become the residual stream (updated in place). The reference's loop (tokquay/model.py:172-181) as five
         launches per block: ``c_attn`` with ``ln_1`` in front, attention, ``c_proj`` adding into x,
-        ``c_fc`` with ``ln_2`` in front and the GELU after, ``mlp.c_proj`` adding into x; then the tied
-        LM head with ``ln_f`` in front (``tq_skinny_linear``)."""
+        ``c_fc`` with ``ln_2`` in front and the GELU after, ``mlp.c_proj`` adding into x
+        (``tq_skinny_linear``); then the tied LM head with ``ln_f`` in front, fused up to
+        ``ops.SKINNY_LM_HEAD_MAX_ROWS`` rows, else ``ln_f`` on its own and the head on hipBLASLt."""
         for i, block in enumerate(self.h):
             at, mlp = block.attn, block.mlp
             qkv = ops.skinny_linear(x, at.c_attn.weight, at.c_attn.bias,
@@ -128,7 +129,10 @@ class GPT2(nn.Module):
             h = ops.skinny_linear(x, mlp.c_fc.weight, mlp.c_fc.bias, ln=(block.ln_2.weight, block.ln_2.bias,
                                                                         block.ln_2.eps), epilogue="gelu")  # fmt: skip
             ops.skinny_linear(h, mlp.c_proj.weight, mlp.c_proj.bias, epilogue="residual", out=x)
-        return ops.skinny_linear(x, self.wte.weight, None, ln=(self.ln_f.weight, self.ln_f.bias, self.ln_f.eps))
+        if x.shape[0] <= ops.SKINNY_LM_HEAD_MAX_ROWS:
+            return ops.skinny_linear(x, self.wte.weight, None, ln=(self.ln_f.weight, self.ln_f.bias, self.ln_f.eps))
+        _, h = ops.add_layernorm(x, None, self.ln_f.weight, self.ln_f.bias, self.ln_f.eps, x_out=x)
+        return h @ self.wte.weight.T
 
     def forward(self, input_ids: torch.Tensor, cache: PagedBatch, last_only: bool = False) -> torch.Tensor:
         """input_ids ``[B, T]`` (new tokens, right-padded) -> logits ``[B, T, vocab]``, or ``[B, 1, vocab]``

@@ -250,6 +250,14 @@ def add_layernorm(x: torch.Tensor, y: torch.Tensor | None, weight: torch.Tensor,
 # (graphs + pipelining, contexts ~300-500): 24 / 32 / 48 / 64 sequences 0.95 / 0.98 / 1.13 / 1.18 ms
 # on hipBLASLt with separate LayerNorm launches, 0.77 / 0.80 / 1.10 / 1.14 ms with it.
 SKINNY_MAX_ROWS = 64
+# The tied LM head (154 MB of weights) stays fused with ln_f only while the rows fit one row block:
+# beyond 16 rows every row group re-reads the weights, and hipBLASLt plus a separate LayerNorm is
+# faster. Decode step p50 at 24 / 32 / 64 sequences 0.73 / 0.74 / 1.08 ms fused, 0.70 / 0.72 / 1.03 ms
+# on the library; at 1 / 8 sequences 0.42 / 0.46 fused, 0.44 / 0.47 on the library (graph-timed
+# back to back, the library looks faster there too, 29.5 vs 39.9 us at 8 rows, but only because
+# repeated calls find the weights in the last-level cache, which a decode step's other 340 MB of
+# weights evict).
+SKINNY_LM_HEAD_MAX_ROWS = 16
 SKINNY_WIDTHS = (768, 3072)
 _EPILOGUES = {"none": 0, "gelu": 1, "residual": 2}
 
