@@ -160,7 +160,28 @@ def test_decode_config4_scale():
     check(sc, brute=False)
 
 
+@pytest.mark.parametrize("block_size", [8, 32])
+def test_decode_full_grid_other_block_sizes(block_size):
+    """256 sequences at contexts U[1, 1024]: the automatic choice is the one-wave-per-sequence grid
+    with the snaked dispatch order, here on the block-size-32 instance and the generic one."""
+    rng = random.Random(block_size + 100)
+    ctx = [rng.randint(1, 1024) for _ in range(256)]
+    sc = Scenario([c - 1 for c in ctx], [1] * 256, block_size=block_size, seed=block_size + 100)
+    check(sc, brute=False)
+
+
 # ------------------------------------------------------------------------------ prefill
+@pytest.mark.parametrize("block_size", [8, 32])
+def test_prefill_ragged_batch_other_block_sizes(block_size):
+    """20 prompts of 1-300 tokens, some continuing at a cached prefix: a launch with several hundred
+    query tiles (key split 2-4) on the block-size-32 instance and the generic one."""
+    rng = random.Random(block_size + 200)
+    starts = [rng.choice([0, 0, 17, 64, 250]) for _ in range(20)]
+    lens = [rng.randint(1, 300) for _ in range(20)]
+    sc = Scenario(starts, lens, block_size=block_size, seed=block_size + 200)
+    check(sc, brute=False)
+
+
 @pytest.mark.parametrize("block_size", [4, 16, 32, 48])
 @pytest.mark.parametrize("start,n", [(0, 2), (0, 15), (0, 16), (0, 17), (0, 100), (5, 40), (16, 16), (250, 300), (0, 1024)])
 def test_prefill_single_sequence(block_size, start, n):
