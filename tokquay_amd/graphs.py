@@ -7,8 +7,9 @@ kernel that also writes the new K/V, LM head, greedy argmax) once per batch
 bucket (powers of two) into a HIP graph and replays it. Buckets of at most 64
 rows run the fused small-batch path (``GPT2.skinny_logits``: each linear of a
 block with its LayerNorm / GELU / residual add in one ``tq_skinny_linear`` launch,
-about 65 launches per step; ``ln_f`` and the LM head on hipBLASLt); larger buckets
-the library GEMMs with ``tq_add_layernorm``.
+about 65 launches per step; the LM head fused with ``ln_f`` up to 16 rows, else
+``ln_f`` alone and the head on hipBLASLt); larger buckets the library GEMMs with
+``tq_add_layernorm``.
 
 What changes between steps lives in static device buffers at fixed addresses,
 refreshed by one host-to-device copy per step: token ids, positions,
