@@ -2,16 +2,30 @@
 
 Workload (the decode-throughput configuration): GPT-2 124M, random-init fp32
 weights (normal std 0.02), 256 concurrent sequences whose context at the last
-timed step is ~ U[256, 1024] (seeded), block size 16, KV pool of 16,384 blocks
-(262,144 slots, 18 GiB). Prompts of random token ids are prefilled through the
-engine (untimed); then W warm-up and K timed decode steps run through
-``Engine.step`` (scheduler + paged forward + sampling + the step's one sync).
+decode step of the run is ~ U[256, 1024] (seeded), block size 16, KV pool of
+16,384 blocks (262,144 slots, 18 GiB). Prompts of random token ids are
+prefilled through the engine (untimed); then W warm-up and K timed decode steps
+run through ``Engine.step`` (scheduler + paged forward + sampling + the step's
+one sync).
 
 Prints one JSON line: decode tok/s (``value``), the decode-attention kernel's
-roofline (algorithmic bytes / live HIP-event kernel time vs 8 TB/s), the
-CPU baseline (the oracle's restatement of the reference gather path on this
-host's cores, a bounded sample of the same state) and, unless ``--no-itl``,
-p50/p99 inter-token latency of the 300-request Poisson serving trace.
+roofline (algorithmic bytes / live HIP-event kernel time vs 8 TB/s), and beside
+them:
+
+* ``cpu_baseline`` / ``gpu_gather_baseline``: the reference's gather-and-attend
+  paged path (the oracle's restatement of it) on this host's CPU cores and, with
+  torch, on the same GPU, from the same state, with greedy-id agreement;
+* ``decode_op_alone``: the decode kernel alone on the 64-sequence op shape;
+* ``prefill``: the prefill kernel's fp32 MFMA utilisation over mixed
+  chunked-prefill + decode steps, and ``mixed_engine``: the same scenario
+  through ``Engine.step`` with chunked prefill and with the reference's
+  alternating policy;
+* ``itl`` / ``itl_chunked`` / ``saturated``: the 300-request serving trace
+  (p50 / p99 inter-token latency) with each policy, and all requests at t=0.
+
+Other modes (each prints one JSON line and exits): ``--small-batch N`` (decode
+step p50 at N sequences), ``--configs`` (the small configurations side by side
+with the gather path), ``--pmc-probe`` (a short run for counter collection).
 """
 
 from __future__ import annotations
@@ -20,7 +34,6 @@ import argparse
 import json
 import math
 import os
-import platform
 import random
 import statistics
 import sys
@@ -34,26 +47,39 @@ METRIC = "decode tok/s (1 GPU); paged-attn HBM GB/s as % of peak; p50 ITL"
 HBM_PEAK_GBS = 8000.0
 MFMA_FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix
 N_SEQS, CTX_LO, CTX_HI, BLOCK, POOL_BLOCKS = 256, 256, 1024, 16, 16384
+N_HEAD, D_HEAD = 12, 64
 # HBM bytes the decode kernel moves per algorithmic byte on this workload, from two rocprofv3
 # counter runs on ``bench.py --pmc-probe`` (FETCH_SIZE scaled x2.0 and WRITE_SIZE x1.0, the factors
 # a 1 GiB copy kernel of known size gives): 933.56 MB read + 2.36 MB written per launch for
 # 921.04 MB algorithmic. The excess is the masked tail of each sequence's last 16-position chunk.
 DECODE_TRAFFIC_PER_ALGO_BYTE = 1.0162
+# Greedy ids may differ from a reference run only where that run picked its token by a top-1 /
+# top-2 logit gap below this (fp32 logits of two implementations differ by a few 1e-6).
+MARGIN_BOUND = 1e-4
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def decode_bytes(ctxs: list[int], n_head: int = 12, d: int = 64, bs: int = BLOCK) -> int:
-    """Algorithmic HBM bytes of one decode-attention layer call (tq_paged_decode_write): every K and
-    V row of the context read once (the new token's from the projection output), the new token's
-    K and V written into the pool, q in and out, the block-table entries and context lengths."""
+def cdiv(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+def decode_bytes(ctxs: list[int], n_head: int = N_HEAD, d: int = D_HEAD, bs: int = BLOCK, write: bool = True) -> int:
+    """Algorithmic HBM bytes of one decode-attention layer call: every K and V row of the context
+    read once, q in and out, the block-table entries and context lengths, and (``write``, the
+    engine's tq_paged_decode_write) the new token's K and V written into the pool."""
     kv = sum(2 * c * n_head * d * 4 for c in ctxs)
-    new_kv = 2 * len(ctxs) * n_head * d * 4
+    new_kv = 2 * len(ctxs) * n_head * d * 4 if write else 0
     qo = 2 * len(ctxs) * n_head * d * 4
-    meta = sum(-(-c // bs) * 4 for c in ctxs) + 4 * len(ctxs)
+    meta = sum(cdiv(c, bs) * 4 for c in ctxs) + 4 * len(ctxs)
     return kv + new_kv + qo + meta
+
+
+def prefill_flops(starts: list[int], lens: list[int], n_head: int = N_HEAD, d: int = D_HEAD) -> int:
+    """Causal-exact flops of one prefill layer call: QK^T and PV over the visible keys only."""
+    return sum(4 * n_head * d * (n * s + n * (n + 1) // 2) for s, n in zip(starts, lens))
 
 
 class LaunchTimer:
@@ -88,9 +114,13 @@ class LaunchTimer:
         return sum(a.elapsed_time(b) for a, b in self.pairs)
 
 
-def prefill_flops(starts: list[int], lens: list[int], n_head: int = 12, d: int = 64) -> int:
-    """Causal-exact flops of one prefill layer call: QK^T and PV over the visible keys only."""
-    return sum(4 * n_head * d * (n * s + n * (n + 1) // 2) for s, n in zip(starts, lens))
+def load_model(seed: int = 0):
+    from tokquay_amd.model import GPT2, GPT2Config
+    from tokquay_amd.weights import random_state_dict
+
+    model = GPT2(GPT2Config())
+    model.load_state_dict(random_state_dict(model.cfg, seed=seed))
+    return model.cuda().eval()
 
 
 def build_engine(steps_needed: int, seed: int = 0):
@@ -98,16 +128,11 @@ def build_engine(steps_needed: int, seed: int = 0):
 
     from tokquay_amd.engine import Engine
     from tokquay_amd.kv_cache import BlockAllocator
-    from tokquay_amd.model import GPT2, GPT2Config
     from tokquay_amd.scheduler import SchedulerConfig
     from tokquay_amd.sequence import SamplingParams
-    from tokquay_amd.weights import random_state_dict
 
-    cfg = GPT2Config()
-    model = GPT2(cfg)
-    model.load_state_dict(random_state_dict(cfg, seed=seed))
-    model = model.cuda().eval()
-    alloc = BlockAllocator(cfg, POOL_BLOCKS, BLOCK, device="cuda")
+    model = load_model(seed)
+    alloc = BlockAllocator(model.cfg, POOL_BLOCKS, BLOCK, device="cuda")
     engine = Engine(model, alloc, SchedulerConfig(max_num_seqs=N_SEQS, max_num_batched_tokens=32768, max_model_len=1024))
     rng = random.Random(seed + 4)
     final_ctx = [rng.randint(CTX_LO, CTX_HI) for _ in range(N_SEQS)]
@@ -119,96 +144,89 @@ def build_engine(steps_needed: int, seed: int = 0):
         engine.step()  # prefill steps (and a few decodes between them)
     torch.cuda.synchronize()
     log(f"prefilled {N_SEQS} sequences in {time.perf_counter() - t0:.2f} s")
-    return engine, model
+    return engine, model, final_ctx
 
 
-def snapshot_for_cpu(engine, seqs, n_cpu: int, spare_per_seq: int):
-    """Copy the first n_cpu running sequences' blocks into a compact CPU pool (oracle layout),
-    with ``spare_per_seq`` empty blocks each for the positions the CPU steps append."""
+def host_cpu_name() -> str:
+    """The host CPU's model name (what ``lscpu`` prints as "Model name", from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or platform.machine()
+
+
+def margin_agreement(got: list[list[int]], want: list[list[int]], margins: list[list[float]]) -> dict:
+    """Per-step greedy ids of two runs fed the same tokens: how many agree, and whether every
+    disagreement sits where the reference run's pick had a top-1 / top-2 gap below MARGIN_BOUND."""
+    total = same = 0
+    near_ties, violations = [], []
+    for s, (g, w, m) in enumerate(zip(got, want, margins)):
+        for i, (a, b, gap) in enumerate(zip(g, w, m)):
+            total += 1
+            if a == b:
+                same += 1
+            else:
+                (near_ties if gap < MARGIN_BOUND else violations).append((s, i, round(gap, 7)))
+    return {"ids_compared": total, "ids_identical": same, "near_tie_mismatches": len(near_ties),
+            "mismatches_above_margin_bound": len(violations), "margin_bound": MARGIN_BOUND,
+            "min_reference_margin": round(min(min(m) for m in margins), 7)}  # fmt: skip
+
+
+# ------------------------------------------------------------------------------ HIP path measurements
+def decode_op_alone(seed: int = 2) -> dict:
+    """The decode kernel alone on the op-alone shape: 64 sequences, 12 heads, head_dim 64,
+    contexts U[16, 512] (redrawn with seeds 0, 1, ... until they fit the 1,024-block pool), block
+    size 16, block tables a seeded random permutation, Q and the pool ~ N(0, 1), one query per
+    sequence; a 1-layer pool. Median of 200 back-to-back launches timed with HIP events."""
     import torch
 
-    pool = engine.allocator.pool
-    picked = seqs[:n_cpu]
-    used = sorted({b for s in picked for b in s.block_table})
-    remap = {b: i for i, b in enumerate(used)}
-    cpu_pool = torch.empty((len(used) + spare_per_seq * len(picked),) + tuple(pool.shape[1:]), dtype=pool.dtype)
-    for i in range(0, len(used), 512):
-        idx = torch.tensor(used[i : i + 512], device=pool.device)
-        cpu_pool[i : i + len(idx)].copy_(pool.index_select(0, idx))
-    spare = iter(range(len(used), cpu_pool.shape[0]))
-    state = []
-    for s in picked:
-        table = [remap[b] for b in s.block_table] + [next(spare) for _ in range(spare_per_seq)]
-        state.append((table, s.num_cached_tokens, list(s.token_ids)))
-    return cpu_pool, state
+    from tokquay_amd import ops
 
-
-def cpu_baseline(cpu_pool, state, weights, steps: int):
-    """Time the oracle (the reference gather-and-attend path, restated) on this host's CPU cores."""
-    import torch
-
-    from oracle.gpt2_ref import RefConfig, build_ref_model
-    from oracle.paged_ref import RefPagedBatch
-
-    threads = torch.get_num_threads()
-    model = build_ref_model(RefConfig(), weights)
-    tables = [list(t) for t, _, _ in state]
-    cached = [c for _, c, _ in state]
-    tokens = [list(t) for _, _, t in state]
-    times, first_ids = [], None
-    for step in range(steps + 1):  # the first step is the warm-up
-        batch = RefPagedBatch(cpu_pool, BLOCK, tables, cached, [1] * len(cached))
-        ids = torch.tensor([[t[c]] for t, c in zip(tokens, cached)])
-        t0 = time.perf_counter()
-        with torch.no_grad():
-            logits = model(ids, batch, last_only=True)[:, 0]
-        nxt = logits.argmax(-1).tolist()
-        dt = time.perf_counter() - t0
-        if step == 0:
-            first_ids = nxt
-        else:
-            times.append(dt)
-        for i, t in enumerate(nxt):
-            tokens[i].append(t)
-            cached[i] += 1
-    med = statistics.median(times)
-    return {"step_s": med, "threads": threads, "first_ids": first_ids, "times": times}
-
-
-def itl_trace(seed: int = 0, rate: float = 8.0, n: int = 300):
-    import torch
-
-    from tokquay_amd.engine import Engine
-    from tokquay_amd.harness import run_trace, summarize
-    from tokquay_amd.kv_cache import BlockAllocator
-    from tokquay_amd.model import GPT2, GPT2Config
-    from tokquay_amd.scheduler import SchedulerConfig
-    from tokquay_amd.weights import random_state_dict
-    from tokquay_amd.workload import make_workload
-
-    cfg = GPT2Config()
-    model = GPT2(cfg)
-    model.load_state_dict(random_state_dict(cfg, seed=seed))
-    model = model.cuda().eval()
-    # Warm-up trace (untimed) so kernels and GEMM heuristics are ready.
-    warm = Engine(model, BlockAllocator(cfg, 1024, 16, device="cuda"))
-    run_trace(warm, make_workload(math.inf, 12, seed=999, prompt_len=(16, 128), output_len=(8, 16)))
-    del warm
+    draw = 0
+    while True:
+        rng = random.Random(draw)
+        ctx = [rng.randint(16, 512) for _ in range(64)]
+        if sum(cdiv(c, BLOCK) for c in ctx) <= 1024:
+            break
+        draw += 1
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    pool = torch.randn(1024, 1, 2, N_HEAD, BLOCK, D_HEAD, device="cuda", generator=g)
+    perm = torch.randperm(1024, device="cuda", generator=g).tolist()
+    tables = torch.zeros(64, max(cdiv(c, BLOCK) for c in ctx), dtype=torch.int32)
+    i = 0
+    for r, c in enumerate(ctx):
+        n = cdiv(c, BLOCK)
+        tables[r, :n] = torch.tensor(perm[i : i + n], dtype=torch.int32)
+        i += n
+    tables = tables.cuda()
+    lens = torch.tensor(ctx, dtype=torch.int32, device="cuda")
+    order = torch.tensor(sorted(range(64), key=lambda r: -ctx[r]), dtype=torch.int32, device="cuda")
+    q = torch.randn(64, N_HEAD * D_HEAD, device="cuda", generator=g)
+    out = torch.empty_like(q)
+    call = lambda: ops.paged_decode(out, q, pool, 0, tables, lens, max(ctx), seq_order=order)  # noqa: E731
+    for _ in range(10):
+        call()
+    times = []
+    for _ in range(200):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        call()
+        b.record()
+        times.append((a, b))
     torch.cuda.synchronize()
-    alloc = BlockAllocator(cfg, 1024, 16, device="cuda")
-    engine = Engine(model, alloc, SchedulerConfig(max_num_seqs=64, max_num_batched_tokens=2048))
-    res = run_trace(engine, make_workload(rate, n, seed=seed))
-    s = summarize(res, alloc.bytes_per_block // 16)
-    return {
-        "requests": s["requests"],
-        "rate_req_s": rate if math.isfinite(rate) else "all at t=0",
-        "throughput_tok_s": round(s["throughput_tok_s"], 1),
-        "itl_p50_ms": round(s["itl_ms"]["p50"], 3),
-        "itl_p99_ms": round(s["itl_ms"]["p99"], 3),
-        "ttft_p50_ms": round(s["ttft_ms"]["p50"], 2),
-        "decode_step_p50_ms": round(s["stalls"].get("decode_step_ms", {}).get("p50", float("nan")), 3),
-        "preemptions": s["stats"]["num_preemptions"],
-    }
+    us = statistics.median(a.elapsed_time(b) for a, b in times) * 1e3
+    nbytes = decode_bytes(ctx, write=False)
+    return {"workload": f"decode op alone: 64 sequences, ctx U[16,512] (draw seed {draw}, {sum(ctx)} positions), "
+                        "12 heads x 64, block 16, 1,024-block pool (1 layer), random block permutation",
+            "draw_seed": draw,
+            "kernel": "tq_paged_decode", "us_per_call": round(us, 2), "bytes_per_call": nbytes,
+            "achieved_GBs": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}  # fmt: skip
 
 
 def mixed_chunked_step(seed: int = 5) -> dict:
@@ -220,15 +238,10 @@ def mixed_chunked_step(seed: int = 5) -> dict:
     from tokquay_amd import kv_cache
     from tokquay_amd.generate import paged_forward
     from tokquay_amd.kv_cache import BlockAllocator
-    from tokquay_amd.model import GPT2, GPT2Config
     from tokquay_amd.sequence import Sequence
-    from tokquay_amd.weights import random_state_dict
 
-    cfg = GPT2Config()
-    model = GPT2(cfg)
-    model.load_state_dict(random_state_dict(cfg, seed=0))
-    model = model.cuda().eval()
-    alloc = BlockAllocator(cfg, 8192, BLOCK, device="cuda")
+    model = load_model()
+    alloc = BlockAllocator(model.cfg, 8192, BLOCK, device="cuda")
     rng = random.Random(seed)
     prompts = [Sequence(i, [rng.randrange(50256) for _ in range(rng.randint(512, 1024))]) for i in range(4)]
     decoders = [Sequence(4 + i, [rng.randrange(50256) for _ in range(rng.randint(64, 768) - 1)]) for i in range(128)]
@@ -278,6 +291,345 @@ def mixed_chunked_step(seed: int = 5) -> dict:
     }
 
 
+def mixed_engine(chunked: bool, seed: int = 5) -> dict:
+    """The mixed scenario through ``Engine.step``: 128 sequences decode (context U[64,768]) when 4
+    prompts of U[512,1024] tokens arrive. With chunked prefill the prompts are fed 256 tokens per
+    step next to the decode rows; with the reference's alternating policy (2,048 padded tokens per
+    step) the prompts are prefilled in steps of their own while the decode rows wait. Reports the
+    steps and wall time until every prompt has its first token, and the longest gap a decoding
+    sequence saw between two tokens meanwhile."""
+    import torch
+
+    from tokquay_amd.engine import Engine
+    from tokquay_amd.kv_cache import BlockAllocator
+    from tokquay_amd.scheduler import SchedulerConfig
+    from tokquay_amd.sequence import SamplingParams
+
+    model = load_model()
+    cfg = SchedulerConfig(max_num_seqs=256, max_num_batched_tokens=2048, chunked_prefill=chunked,
+                          prefill_chunk_tokens=256)  # fmt: skip
+    engine = Engine(model, BlockAllocator(model.cfg, 8192, BLOCK, device="cuda"), cfg)
+    rng = random.Random(seed)
+    prompts = [[rng.randrange(50256) for _ in range(rng.randint(512, 1024))] for _ in range(4)]
+    for _ in range(128):
+        engine.add_request([rng.randrange(50256) for _ in range(rng.randint(64, 768) - 1)],
+                           SamplingParams(max_tokens=128, ignore_eos=True))  # fmt: skip
+    while engine.scheduler.waiting or any(s.num_uncached_tokens > 1 for s in engine.scheduler.running):
+        engine.step()
+    for _ in range(8):  # decode steps: graphs captured, pipeline in steady state
+        engine.step()
+    decoders = {s.seq_id for s in engine.scheduler.running}
+    long_ids = {engine.add_request(p, SamplingParams(max_tokens=1, ignore_eos=True)).seq_id for p in prompts}
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    last: dict[int, float | None] = {i: None for i in decoders}
+    worst_gap, steps, pending = 0.0, 0, set(long_ids)
+    while pending:
+        events = engine.step()
+        now = time.perf_counter()
+        steps += 1
+        for ev in events:
+            pending.discard(ev.seq_id)
+            if ev.seq_id in last:
+                if last[ev.seq_id] is not None:
+                    worst_gap = max(worst_gap, now - last[ev.seq_id])
+                last[ev.seq_id] = now
+    elapsed = time.perf_counter() - t0
+    engine.drain()
+    engine.allocator.check_device_errors()
+    return {"policy": "chunked prefill (256-token chunks)" if chunked else "alternating (reference)",
+            "steps_until_prompts_done": steps, "ms_until_prompts_done": round(elapsed * 1e3, 2),
+            "max_decode_gap_ms": round(worst_gap * 1e3, 2)}  # fmt: skip
+
+
+def itl_trace(seed: int = 0, rate: float = 8.0, n: int = 300, chunked: bool = False) -> dict:
+    import torch
+
+    from tokquay_amd.engine import Engine
+    from tokquay_amd.harness import run_trace, summarize
+    from tokquay_amd.kv_cache import BlockAllocator
+    from tokquay_amd.scheduler import SchedulerConfig
+    from tokquay_amd.workload import make_workload
+
+    model = load_model(seed)
+    cfg = SchedulerConfig(max_num_seqs=64, max_num_batched_tokens=2048, chunked_prefill=chunked)
+    # Warm-up trace (untimed) so kernels, graphs and library heuristics are ready.
+    warm = Engine(model, BlockAllocator(model.cfg, 1024, 16, device="cuda"), cfg)
+    run_trace(warm, make_workload(math.inf, 12, seed=999, prompt_len=(16, 128), output_len=(8, 16)))
+    del warm
+    torch.cuda.synchronize()
+    alloc = BlockAllocator(model.cfg, 1024, 16, device="cuda")
+    engine = Engine(model, alloc, cfg)
+    res = run_trace(engine, make_workload(rate, n, seed=seed))
+    s = summarize(res, alloc.bytes_per_block // 16)
+    st = s["stalls"]
+    out = {
+        "requests": s["requests"],
+        "rate_req_s": rate if math.isfinite(rate) else "all at t=0",
+        "policy": "chunked prefill" if chunked else "alternating (reference)",
+        "throughput_tok_s": round(s["throughput_tok_s"], 1),
+        "itl_p50_ms": round(s["itl_ms"]["p50"], 3),
+        "itl_p99_ms": round(s["itl_ms"]["p99"], 3),
+        "ttft_p50_ms": round(s["ttft_ms"]["p50"], 2),
+        "ttft_p99_ms": round(s["ttft_ms"]["p99"], 2),
+        "decode_step_p50_ms": round(st.get("decode_step_ms", {}).get("p50", float("nan")), 3),
+        "preemptions": s["stats"]["num_preemptions"],
+    }
+    if "frac_gaps_stalled_by_prefill" in st:
+        out["gaps_with_a_prefill_step"] = round(st["frac_gaps_stalled_by_prefill"], 4)
+        out["itl_clean_p50_p99_ms"] = [round(st["itl_ms_clean"]["p50"], 3), round(st["itl_ms_clean"]["p99"], 3)]
+        out["itl_stalled_p50_p99_ms"] = [round(st["itl_ms_stalled"]["p50"], 3), round(st["itl_ms_stalled"]["p99"], 3)]
+    return out
+
+
+def small_batch(nseqs: int, steps: int, prompt: int = 300) -> dict:
+    """Decode-step wall time at a small batch: ``nseqs`` sequences with ``prompt``-token prompts of
+    random ids decode ``steps`` greedy tokens each (graph replay + pipelining, the engine's
+    default). Steps are timed with perf_counter around ``Engine.step()``; the first and last five
+    are dropped."""
+    import torch
+
+    from tokquay_amd.engine import Engine
+    from tokquay_amd.kv_cache import BlockAllocator
+    from tokquay_amd.scheduler import SchedulerConfig
+    from tokquay_amd.sequence import SamplingParams
+
+    model = load_model()
+    engine = Engine(model, BlockAllocator(model.cfg, 4096, BLOCK, device="cuda"),
+                    SchedulerConfig(max_model_len=1024, max_num_seqs=max(nseqs, 1)))  # fmt: skip
+    rng = random.Random(0)
+    for _ in range(nseqs):
+        engine.add_request([rng.randrange(50256) for _ in range(prompt)], SamplingParams(max_tokens=steps, ignore_eos=True))
+    times = []
+    with torch.no_grad():
+        while engine.has_unfinished():
+            t0 = time.perf_counter()
+            engine.step()
+            times.append(time.perf_counter() - t0)
+    kept = times[5:-5]
+    return {"mode": "small-batch decode steps", "sequences": nseqs, "prompt_tokens": prompt, "steps": len(times),
+            "step_p50_ms": round(statistics.median(kept) * 1e3, 3),
+            "step_p99_ms": round(float(sorted(kept)[int(0.99 * (len(kept) - 1))]) * 1e3, 3)}  # fmt: skip
+
+
+# ------------------------------------------------------------------------------ baseline leg
+# The reference's own algorithm (the oracle's restatement of tokquay's gather-and-attend paged
+# path, tokquay/kv_cache.py:228-242 and tokquay/model.py:94-96), timed beside the HIP path. It is
+# the baseline being compared against, never part of what `value` measures.
+def snapshot_for_cpu(engine, seqs, n_cpu: int, spare_per_seq: int):
+    """Copy the first n_cpu running sequences' blocks into a compact CPU pool (oracle layout),
+    with ``spare_per_seq`` empty blocks each for the positions the CPU steps append."""
+    import torch
+
+    pool = engine.allocator.pool
+    picked = seqs[:n_cpu]
+    used = sorted({b for s in picked for b in s.block_table})
+    remap = {b: i for i, b in enumerate(used)}
+    cpu_pool = torch.empty((len(used) + spare_per_seq * len(picked),) + tuple(pool.shape[1:]), dtype=pool.dtype)
+    for i in range(0, len(used), 512):
+        idx = torch.tensor(used[i : i + 512], device=pool.device)
+        cpu_pool[i : i + len(idx)].copy_(pool.index_select(0, idx))
+    spare = iter(range(len(used), cpu_pool.shape[0]))
+    state = []
+    for s in picked:
+        table = [remap[b] for b in s.block_table] + [next(spare) for _ in range(spare_per_seq)]
+        state.append((table, s.num_cached_tokens, list(s.token_ids)))
+    return cpu_pool, state
+
+
+def baseline_cpu(cpu_pool, state, weights, steps: int) -> dict:
+    """Time the oracle gather path on this host's CPU cores: ``steps`` decode steps after one
+    warm-up, each sequence feeding the token it picked in the previous step."""
+    import torch
+
+    from oracle.gpt2_ref import RefConfig, build_ref_model
+    from oracle.paged_ref import RefPagedBatch
+
+    threads = torch.get_num_threads()
+    model = build_ref_model(RefConfig(), weights)
+    tables = [list(t) for t, _, _ in state]
+    cached = [c for _, c, _ in state]
+    tokens = [list(t) for _, _, t in state]
+    times, first_ids, first_margins = [], None, None
+    for step in range(steps + 1):  # the first step is the warm-up
+        batch = RefPagedBatch(cpu_pool, BLOCK, tables, cached, [1] * len(cached))
+        ids = torch.tensor([[t[c]] for t, c in zip(tokens, cached)])
+        t0 = time.perf_counter()
+        with torch.no_grad():
+            logits = model(ids, batch, last_only=True)[:, 0]
+        nxt = logits.argmax(-1).tolist()
+        dt = time.perf_counter() - t0
+        if step == 0:
+            first_ids = nxt
+            top2 = logits.topk(2, dim=-1).values
+            first_margins = (top2[:, 0] - top2[:, 1]).tolist()
+        else:
+            times.append(dt)
+        for i, t in enumerate(nxt):
+            tokens[i].append(t)
+            cached[i] += 1
+    return {"step_s": statistics.median(times), "threads": threads, "first_ids": first_ids,
+            "first_margins": first_margins}  # fmt: skip
+
+
+def baseline_gpu_gather(pool, state, tables_after, hip_steps: list[list[int]], weights, steps: int) -> dict:
+    """The oracle gather path with torch on the GPU, from the state the HIP engine's first measured
+    step started from (``state``: block table, cached positions, tokens per sequence; the pool holds
+    every position cached then). Step j feeds the token the HIP engine picked at its step j - 1, so
+    the two runs see the same inputs every step; its ids are compared with the HIP engine's step j
+    under the margin rule. Blocks for the new positions are the ones the engine used
+    (``tables_after``). Timed: ``steps`` steps after one warm-up, median."""
+    import torch
+
+    from oracle.gpt2_ref import RefConfig, build_ref_model
+    from oracle.paged_ref import RefPagedBatch
+
+    model = build_ref_model(RefConfig(), weights, device="cuda")
+    n = len(state)
+    cached = [c for _, c, _ in state]
+    feed = [t[c] for _, c, t in state]
+    got, margins, times = [], [], []
+    for step in range(steps + 1):
+        tables = [full[: cdiv(c + 1, BLOCK)] for full, c in zip(tables_after, cached)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        with torch.no_grad():
+            batch = RefPagedBatch(pool, BLOCK, tables, cached, [1] * n)
+            ids = torch.tensor([[t] for t in feed], device="cuda")
+            logits = model(ids, batch, last_only=True)[:, 0]
+            nxt = logits.argmax(-1).tolist()
+        times.append(time.perf_counter() - t0)
+        top2 = logits.topk(2, dim=-1).values
+        margins.append((top2[:, 0] - top2[:, 1]).tolist())
+        got.append(nxt)
+        feed = hip_steps[step]  # teacher forcing: the HIP engine's pick is the next input
+        cached = [c + 1 for c in cached]
+    step_s = statistics.median(times[1:])
+    agree = margin_agreement(hip_steps[: steps + 1], got, margins)
+    return {"value": round(n / step_s, 1), "unit": "tok/s", "step_ms": round(step_s * 1e3, 3),
+            "kind": "port", "sample": f"{steps} decode steps (median, after 1 warm-up) of all {n} sequences from the "
+            "HIP run's state, oracle gather-and-attend path (write + gather + masked softmax) in fp32 torch on "
+            "this GPU, fed the HIP engine's tokens", "greedy_ids": agree}  # fmt: skip
+
+
+def baseline_configs() -> list[dict]:
+    """The small configurations side by side: HIP path vs the gather path on this GPU and on this
+    host's CPU cores (``--configs``)."""
+    import torch
+
+    from oracle.gpt2_ref import RefAllocator, RefConfig, build_ref_model, ref_paged_greedy_generate
+    from oracle.paged_ref import RefPagedBatch, ref_attention
+    from tokquay_amd import ops
+    from tokquay_amd.generate import paged_forward, paged_greedy_generate
+    from tokquay_amd.kv_cache import BlockAllocator
+    from tokquay_amd.sequence import Sequence
+    from tokquay_amd.weights import random_state_dict
+
+    def timed(fn, reps, sync=True):
+        out = []
+        for _ in range(reps):
+            if sync:
+                torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            fn()
+            if sync:
+                torch.cuda.synchronize()
+            out.append(time.perf_counter() - t0)
+        return statistics.median(out)
+
+    rows = [{"cpu": host_cpu_name(), "cpu_threads": torch.get_num_threads()}]
+    sd = random_state_dict(load_model().cfg, seed=0)
+    m = load_model()
+
+    # Config 1: 8 prompts U[16,64], 32 greedy tokens each, pool 256 blocks.
+    rng = random.Random(1)
+    prompts = [[rng.randrange(50256) for _ in range(rng.randint(16, 64))] for _ in range(8)]
+    paged_greedy_generate(m, BlockAllocator(m.cfg, 256, BLOCK, device="cuda"), prompts, 4)  # warm-up
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    got = paged_greedy_generate(m, BlockAllocator(m.cfg, 256, BLOCK, device="cuda"), prompts, 32)
+    torch.cuda.synchronize()
+    hip_s = time.perf_counter() - t0
+    ref_t = {}
+    for dev in ("cuda", "cpu"):
+        ref = build_ref_model(RefConfig(), sd, device=dev)
+        ref_paged_greedy_generate(ref, RefAllocator(RefConfig(), 256, BLOCK, device=dev), prompts, 2)
+        ref_t[dev] = timed(lambda: ref_paged_greedy_generate(ref, RefAllocator(RefConfig(), 256, BLOCK, device=dev),
+                                                             prompts, 32), 1, sync=dev == "cuda")  # fmt: skip
+    want = ref_paged_greedy_generate(build_ref_model(RefConfig(), sd), RefAllocator(RefConfig(), 256, BLOCK), prompts, 32)
+    rows.append({"config": 1, "hip_s": round(hip_s, 4), "gather_gpu_s": round(ref_t["cuda"], 4),
+                 "gather_cpu_s": round(ref_t["cpu"], 3), "ids_identical_to_cpu_oracle": got == want})  # fmt: skip
+
+    # Config 2: the decode op alone (HIP figures from decode_op_alone, same draw).
+    op = decode_op_alone()
+    rng = random.Random(op["draw_seed"])
+    ctx = [rng.randint(16, 512) for _ in range(64)]
+    g = torch.Generator().manual_seed(2)
+    pool = torch.randn(1024, 1, 2, N_HEAD, BLOCK, D_HEAD, generator=g)
+    perm = torch.randperm(1024, generator=g).tolist()
+    tables, i = [], 0
+    for c in ctx:
+        tables.append(perm[i : i + cdiv(c, BLOCK)])
+        i += cdiv(c, BLOCK)
+    q = torch.randn(64, N_HEAD, 1, D_HEAD, generator=g)
+    t = {}
+    for dev in ("cuda", "cpu"):
+        p, qq = pool.to(dev), q.to(dev)
+        batch = RefPagedBatch(p, BLOCK, tables, [c - 1 for c in ctx], [1] * 64)
+
+        def step():
+            k, v = batch.gather(0)
+            return ref_attention(qq, k, v, batch.mask)
+
+        step()
+        t[dev] = timed(step, 20, sync=dev == "cuda")
+    rows.append({"config": 2, "hip_us": op["us_per_call"], "hip_GBs": op["achieved_GBs"],
+                 "gather_gpu_us": round(t["cuda"] * 1e6, 1), "gather_cpu_us": round(t["cpu"] * 1e6, 1)})  # fmt: skip
+
+    # Config 5: one mixed step (chunk 1 of 4 prompts U[512,1024] next to 128 decode rows).
+    rng = random.Random(5)
+    plen = [rng.randint(512, 1024) for _ in range(4)]
+    dctx = [rng.randint(64, 768) for _ in range(128)]
+    alloc = BlockAllocator(m.cfg, 8192, BLOCK, device="cuda")
+    pr = [Sequence(i, [rng.randrange(50256) for _ in range(n)]) for i, n in enumerate(plen)]
+    de = [Sequence(4 + i, [rng.randrange(50256) for _ in range(c - 1)]) for i, c in enumerate(dctx)]
+    for s in pr + de:
+        alloc.allocate(s)
+    for i in range(0, 128, 32):
+        nxt = paged_forward(m, alloc, de[i : i + 32]).argmax(-1).tolist()
+        for s, tok in zip(de[i : i + 32], nxt):
+            s.append_token(tok)
+            alloc.append_slot(s)
+    paged_forward(m, alloc, pr, [256] * 4)  # chunk 0
+    tables = [list(s.block_table) for s in pr + de]
+    starts = [s.num_cached_tokens for s in pr + de]
+    lens = [256] * 4 + [1] * 128
+    ids = [s.token_ids[st : st + n] for s, st, n in zip(pr + de, starts, lens)]
+    pool_copy = alloc.pool.clone()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    paged_forward(m, alloc, pr + de, lens)
+    torch.cuda.synchronize()
+    hip_ms = (time.perf_counter() - t0) * 1e3
+    t = {}
+    for dev in ("cuda", "cpu"):
+        ref = build_ref_model(RefConfig(), sd, device=dev)
+        p = pool_copy if dev == "cuda" else pool_copy.cpu()
+
+        def step():
+            batch = RefPagedBatch(p, BLOCK, tables, starts, lens)
+            x = torch.tensor([r + [0] * (256 - len(r)) for r in ids], device=dev)
+            with torch.no_grad():
+                return ref(x, batch, last_only=True)
+
+        step()
+        t[dev] = timed(step, 3 if dev == "cuda" else 1, sync=dev == "cuda")
+    rows.append({"config": 5, "chunk": 1, "hip_step_ms": round(hip_ms, 2), "gather_gpu_step_ms": round(t["cuda"] * 1e3, 2),
+                 "gather_cpu_step_s": round(t["cpu"], 2)})  # fmt: skip
+    return rows
+
+
+# ------------------------------------------------------------------------------ main
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -286,8 +638,14 @@ def main() -> int:
     ap.add_argument("--partition-tokens", type=int, default=0, help="decode partition size (0: automatic)")
     ap.add_argument("--cpu-seqs", type=int, default=256, help="sequences in the CPU baseline sample (0: skip)")
     ap.add_argument("--cpu-steps", type=int, default=4, help="timed CPU baseline steps (after one warm-up)")
-    ap.add_argument("--no-itl", action="store_true", help="skip the 300-request serving trace")
-    ap.add_argument("--no-prefill", action="store_true", help="skip the mixed chunked-prefill measurement")
+    ap.add_argument("--gather-steps", type=int, default=3, help="timed GPU gather-path steps (0: skip)")
+    ap.add_argument("--no-itl", action="store_true", help="skip the 300-request serving traces")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the mixed chunked-prefill measurements")
+    ap.add_argument("--small-batch", type=int, default=0, metavar="N",
+                    help="only measure decode-step wall time at N sequences (300-token prompts) and exit")
+    ap.add_argument("--small-batch-steps", type=int, default=80, help="tokens per sequence for --small-batch")
+    ap.add_argument("--configs", action="store_true",
+                    help="only run the small configurations beside the gather path (GPU and CPU) and exit")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="run 3 copies of a known size (1 GiB read + 1 GiB write) and 3 decode steps, then exit; "
                     "for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")  # fmt: skip
@@ -302,10 +660,18 @@ def main() -> int:
     from tokquay_amd.weights import random_state_dict
 
     torch.manual_seed(0)
+    if args.small_batch:
+        print(json.dumps(small_batch(args.small_batch, args.small_batch_steps)), flush=True)
+        return 0
+    if args.configs:
+        for row in baseline_configs():
+            print(json.dumps(row), flush=True)
+        return 0
+
     # Warm-up, timed graph-replayed steps, eager kernel-timing steps, and the few steps the
     # pipelined engine launches ahead or drains around them.
     steps_needed = args.warmup + 2 * args.steps + 4
-    engine, model = build_engine(steps_needed)
+    engine, model, drawn_ctx = build_engine(steps_needed)
     engine.allocator.decode_partition_tokens = args.partition_tokens
 
     for _ in range(args.warmup):
@@ -325,6 +691,9 @@ def main() -> int:
         return 0
     running = list(engine.scheduler.running)
     assert len(running) == N_SEQS, f"{len(running)} sequences running, expected {N_SEQS}"
+    # The state the next step starts from: the baselines start from it too.
+    state = [(list(s.block_table), s.num_cached_tokens, list(s.token_ids)) for s in running]
+    order = {s.seq_id: i for i, s in enumerate(running)}
 
     cpu_state = None
     if args.cpu_seqs > 0:
@@ -332,23 +701,36 @@ def main() -> int:
         cpu_state = snapshot_for_cpu(engine, running, args.cpu_seqs, spare_per_seq=args.cpu_steps // 16 + 2)
         log(f"copied {cpu_state[0].shape[0]} blocks for the CPU sample in {time.perf_counter() - t0:.1f} s")
 
-    # The step after the CPU snapshot (its ids are what the CPU sample's first step must give).
-    # The engine launches the following step ahead, so the timed region starts in steady state.
-    first_ids = [e.token_id for e in engine.step()]
+    def by_row(events) -> list[int]:
+        ids = [0] * N_SEQS
+        for ev in events:
+            ids[order[ev.seq_id]] = ev.token_id
+        return ids
+
+    # The step after the snapshot. The engine launches the following step ahead, so the timed
+    # region starts in steady state.
+    hip_steps = [by_row(engine.step())]
 
     # Timed region: K decode steps through Engine.step, replayed from the captured HIP graph.
     # The step in flight at the start is finished before the clock starts; the step launched
     # ahead by the last call is finished inside it: K steps of GPU work, K steps of tokens.
+    # Context of each row in the first step of GPU work inside the timed region (the step launched
+    # ahead is already counted in num_cached_tokens).
+    timed_ctx = [s.num_cached_tokens + 1 for s in running]
+    below = sorted({d - c for d, c in zip((drawn_ctx[s.seq_id] for s in running), timed_ctx)})
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    emitted = 0
+    emitted = []
     for k in range(args.steps):
-        emitted += len(engine.step())
+        emitted.append(engine.step())
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    assert emitted == N_SEQS * args.steps, emitted
+    n_tokens = sum(len(e) for e in emitted)
+    assert n_tokens == N_SEQS * args.steps, n_tokens
+    hip_steps += [by_row(e) for e in emitted]
     ms_per_step = elapsed * 1e3 / args.steps
-    tok_s = emitted / elapsed
+    tok_s = n_tokens / elapsed
+    mean_ctx_timed = statistics.mean(timed_ctx) + (args.steps - 1) / 2
     engine.drain()
 
     # Kernel timing: K more decode steps run eagerly, every decode launch timed by HIP events
@@ -387,17 +769,21 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic: random-init weights (seed 0), random token ids",
         "config": {
-            "workload": "scaled decode: GPT-2 124M fp32, 256 concurrent sequences, context U[256,1024], "
-            "block_size 16, pool 16384 blocks (262144 slots)",
+            "workload": "scaled decode: GPT-2 124M fp32, 256 concurrent sequences, block_size 16, pool 16384 blocks "
+            "(262144 slots); contexts drawn U[256,1024] are each sequence's context after the run's last decode "
+            f"step, so the timed steps run {min(below) - args.steps + 1} to {max(below)} positions below the "
+            f"draws: mean context {mean_ctx_timed:.1f} over the timed steps (the draws' mean: "
+            f"{statistics.mean(drawn_ctx):.1f})",
             "num_seqs": N_SEQS,
             "block_size": BLOCK,
             "pool_blocks": POOL_BLOCKS,
+            "timed_mean_context": round(mean_ctx_timed, 1),
             "decode_partition_tokens": args.partition_tokens,
             "decode_steps": "HIP-graph replay (one graph per batch bucket); roofline from the same shape run eagerly",
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "tq_paged_decode (decode_partition_kernel; decode_merge_kernel when a sequence spans several partitions)",
+            "kernel": "tq_paged_decode_write (decode_partition_kernel; decode_merge_kernel when a sequence spans several partitions)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -411,33 +797,46 @@ def main() -> int:
         },
     }
 
+    weights = random_state_dict(model.cfg, seed=0)
+    if args.gather_steps > 0:
+        log(f"GPU gather baseline: {N_SEQS} sequences, {args.gather_steps} timed steps ...")
+        tables_after = [list(s.block_table) for s in running]
+        gb = baseline_gpu_gather(engine.allocator.pool, state, tables_after, hip_steps, weights, args.gather_steps)
+        gb["speedup_of_hip_engine"] = round(tok_s / gb["value"], 2)
+        result["gpu_gather_baseline"] = gb
     if cpu_state is not None:
-        cpu_pool, state = cpu_state
-        log(f"CPU baseline: {len(state)} sequences, {args.cpu_steps} timed steps ...")
-        cb = cpu_baseline(cpu_pool, state, random_state_dict(model.cfg, seed=0), args.cpu_steps)
-        n = len(state)
-        match = sum(int(a == b) for a, b in zip(cb["first_ids"], first_ids[:n])) / n
+        cpu_pool, cstate = cpu_state
+        log(f"CPU baseline: {len(cstate)} sequences, {args.cpu_steps} timed steps ...")
+        cb = baseline_cpu(cpu_pool, cstate, weights, args.cpu_steps)
+        n = len(cstate)
+        agree = margin_agreement([hip_steps[0][:n]], [cb["first_ids"]], [cb["first_margins"]])
         result["cpu_baseline"] = {
             "value": round(n / cb["step_s"], 2),
             "unit": "tok/s",
             "cores": cb["threads"],
             "kind": "port",
             "sample": f"{args.cpu_steps} decode steps (median, after 1 warm-up) of {n} of the 256 sequences from the "
-            f"same state, oracle gather-and-attend path in fp32 torch on {cb['threads']} threads "
-            f"({platform.processor() or platform.machine()})",
+            f"same state, oracle gather-and-attend path in fp32 torch on {cb['threads']} threads",
+            "cpu_model": host_cpu_name(),
             "step_s": round(cb["step_s"], 3),
-            "greedy_ids_match_gpu": match,
+            "greedy_ids_first_step": agree,
         }
         del cpu_pool
     del engine, graphs
     torch.cuda.empty_cache()
+    log("decode op alone (64 sequences, ctx U[16,512]) ...")
+    result["decode_op_alone"] = decode_op_alone()
     if not args.no_prefill:
         log("mixed chunked-prefill + decode steps ...")
         result["prefill"] = mixed_chunked_step()
         log(f"prefill: {result['prefill']['achieved']} TFLOP/s = {result['prefill']['frac']:.3f} of fp32 MFMA peak")
+        result["mixed_engine"] = [mixed_engine(chunked=True), mixed_engine(chunked=False)]
+        torch.cuda.empty_cache()
     if not args.no_itl:
-        log("serving trace: 300 requests, Poisson 8 req/s ...")
+        log("serving trace: 300 requests, Poisson 8 req/s, alternating policy ...")
         result["itl"] = itl_trace()
+        log("serving trace: 300 requests, Poisson 8 req/s, chunked prefill ...")
+        result["itl_chunked"] = itl_trace(chunked=True)
         log("saturated trace: the same 300 requests, all arriving at t=0 ...")
         sat = itl_trace(rate=math.inf)
         # The reference's saturated-throughput run (Documentation/results.md:97-101): same workload

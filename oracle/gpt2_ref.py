@@ -224,16 +224,26 @@ def ref_paged_greedy_generate(model: RefGPT2, alloc: RefAllocator, prompts, max_
 
 
 @torch.no_grad()
-def ref_greedy_generate(model: RefGPT2, prompt: list[int], max_new_tokens: int) -> list[int]:
-    """Batch-of-one greedy decode on the contiguous cache (tokquay/generate.py:17-49)."""
+def ref_greedy_generate(model: RefGPT2, prompt: list[int], max_new_tokens: int,
+                        margins: list[float] | None = None) -> list[int]:  # fmt: skip
+    """Batch-of-one greedy decode on the contiguous cache (tokquay/generate.py:17-49). If
+    ``margins`` is given, appends each pick's top-1 minus top-2 logit gap."""
     dtype = next(model.parameters()).dtype
     device = next(model.parameters()).device
     ids = torch.tensor([prompt], device=device)
     cache = RefContiguousKVCache(model.cfg, 1, len(prompt) + max_new_tokens, device=device, dtype=dtype)
-    nxt = model(ids, cache, last_only=True)[:, -1].argmax(-1, keepdim=True)
+
+    def pick(logits: torch.Tensor) -> torch.Tensor:
+        row = logits[:, -1]
+        if margins is not None:
+            top2 = row[0].topk(2).values
+            margins.append(float(top2[0] - top2[1]))
+        return row.argmax(-1, keepdim=True)
+
+    nxt = pick(model(ids, cache, last_only=True))
     out = [int(nxt)]
     for _ in range(max_new_tokens - 1):
-        nxt = model(nxt, cache, last_only=True)[:, -1].argmax(-1, keepdim=True)
+        nxt = pick(model(nxt, cache, last_only=True))
         out.append(int(nxt))
     return out
 

@@ -12,16 +12,7 @@ import pytest
 import torch
 
 from tokquay_amd.engine import EngineStats, KVSnapshot, StepInfo, TokenEvent, sample_token
-from tokquay_amd.harness import (
-    RequestRecord,
-    RunResult,
-    StepRecord,
-    inter_token_gaps,
-    percentiles,
-    prefill_stall_analysis,
-    run_trace,
-    summarize,
-)
+from tokquay_amd.harness import TraceLog, percentiles, prefill_stall_analysis, run_trace, summarize, token_gaps
 from tokquay_amd.sequence import SamplingParams
 from tokquay_amd.workload import VOCAB_SIZE, RequestSpec, make_workload
 
@@ -115,10 +106,11 @@ def scenario():
 
 
 def test_tokens_are_stamped_when_their_step_ends():
-    r0, r1, r2 = scenario().requests
-    assert r0.token_times == pytest.approx([0.5, 1.1, 1.2])
-    assert r1.token_times == pytest.approx([1.0, 1.1])
-    assert r2.token_times == pytest.approx([5.5])
+    log = scenario()
+    assert log.request_token_times(0) == pytest.approx([0.5, 1.1, 1.2])
+    assert log.request_token_times(1) == pytest.approx([1.0, 1.1])
+    assert log.request_token_times(2) == pytest.approx([5.5])
+    assert log.request_token_ids(0) == [7, 7, 7]
 
 
 def test_summary_metrics_match_a_hand_calculation():
@@ -142,12 +134,13 @@ def test_stall_analysis_splits_gaps_by_prefill():
 
 
 def test_prefill_cost_per_token_is_recovered():
-    recs, t = [], 0.0
+    log, t = TraceLog(arrivals=[0.0], prompt_lens=[1], output_lens=[2]), 0.0
     for tokens in (100, 400, 900, 2000):
         dur = (20 + 0.05 * tokens) / 1e3
-        recs.append(StepRecord(t, t + dur, True, 1, tokens, 0, 0, 1))
+        log.steps.append((t, t + dur, True, 1, tokens, 0, 0, 1))
         t += dur
-    out = prefill_stall_analysis(RunResult([RequestRecord(0.0, 1, 2, [0.1, 0.2])], recs, {}, t))
+    log.token_request, log.token_step, log.token_ids = [0, 0], [0, 1], [5, 6]
+    out = prefill_stall_analysis(log)
     assert out["prefill_ms_per_padded_token"] == pytest.approx(0.05) and out["prefill_ms_fixed"] == pytest.approx(20)
 
 
@@ -155,7 +148,7 @@ def test_percentiles_and_gaps():
     p = percentiles(list(range(1, 101)))
     assert p == {"p50": pytest.approx(50.5), "p99": pytest.approx(99.01), "mean": pytest.approx(50.5)}
     assert all(math.isnan(v) for v in percentiles([]).values())
-    assert list(inter_token_gaps(scenario())[2].round(3)) == [0.6, 0.1, 0.1]
+    assert list(token_gaps(scenario())[2].round(3)) == [0.6, 0.1, 0.1]
 
 
 def test_a_stuck_system_raises():

@@ -120,6 +120,16 @@ def test_validation_order_and_messages(nat):
         PagedBatch(pool, 4, [[0], [1]], [0, 4], [1, 1])
     with pytest.raises((ValueError, OverflowError)):
         PagedBatch(pool, 4, [[2**31]], [0], [1])
+    # A start near the top of int64: the context sum must not wrap (it would pass the table check).
+    with pytest.raises(ValueError, match=rf"sequence 0: 1 blocks cannot hold {2**62 + 1} tokens"):
+        PagedBatch(pool, 4, [[0]], [2**62], [1])
+    with pytest.raises(ValueError, match=rf"sequence 0: 1 blocks cannot hold {2**63 + 2**62} tokens"):
+        PagedBatch(pool, 4, [[0]], [2**63 - 1], [2**62 + 1])
+    # Past int32 (the kernels' position type) even when the table is long enough.
+    with pytest.raises(ValueError, match="int32 positions"):
+        PagedBatch(pool, 1024, [[0] * (2**21 + 1)], [2**31 - 1], [1])
+    # The last context the kernels take is accepted.
+    assert PagedBatch(pool, 1024, [[0] * 2**21], [2**31 - 2], [1]).max_ctx == 2**31 - 1
     with pytest.raises(ValueError, match="do not match"):
         h = torch.empty(100, dtype=torch.int64)
         nat.fill([[0]], [0], [1], 4, h.data_ptr(), 3, h.data_ptr(), 50)

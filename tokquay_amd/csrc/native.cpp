@@ -92,7 +92,21 @@ bool make_plan(PyObject* tables, PyObject* start, PyObject* new_lens, int64_t bs
       PyErr_SetString(PyExc_TypeError, "every block table must be a list");
       return false;
     }
-    const int64_t ctx = s + n;
+    // s >= 0 and n >= 1 here, so the sum is exact in 64 unsigned bits; the kernels take int32
+    // positions, so a context past INT32_MAX is refused before anything is sized from it.
+    const uint64_t ctx_u = (uint64_t)s + (uint64_t)n;
+    if (ctx_u > (uint64_t)INT32_MAX) {
+      const uint64_t need_u = ctx_u / (uint64_t)bs + (ctx_u % (uint64_t)bs != 0);
+      if ((uint64_t)PyList_GET_SIZE(tbl) < need_u) {
+        PyErr_Format(PyExc_ValueError, "sequence %zd: %zd blocks cannot hold %llu tokens", b, PyList_GET_SIZE(tbl),
+                     (unsigned long long)ctx_u);
+      } else {
+        PyErr_Format(PyExc_ValueError, "sequence %zd: %llu tokens exceed the kernels' int32 positions", b,
+                     (unsigned long long)ctx_u);
+      }
+      return false;
+    }
+    const int64_t ctx = (int64_t)ctx_u;
     const int64_t need = cdiv(ctx, bs);
     if (PyList_GET_SIZE(tbl) < need) {
       PyErr_Format(PyExc_ValueError, "sequence %zd: %zd blocks cannot hold %lld tokens", b, PyList_GET_SIZE(tbl),

@@ -365,45 +365,24 @@ def embed_rows(ids: torch.Tensor, positions: torch.Tensor, wte: torch.Tensor, wp
 
 
 # ------------------------------------------------------------------------------ library GEMMs
-# hipBLASLt's default fp32 kernel for a given shape depends on the operand layout, and for some
-# row counts the transposed-weight ("NN") call is clearly faster: at 256 rows, c_attn
-# ([768] -> [2304]) 15.8 -> 12.8 us and c_fc (+ GELU, [768] -> [3072]) 16.7 -> 13.7 us, while at
-# 224 or 320 rows, and for the [3072] -> [768] projection at any, the weight as stored ("TN") is
-# as fast or faster. Which layout a launch uses is therefore measured on the device, once per
-# (rows, out, in, epilogue), for the power-of-two row counts decode steps are captured at.
-_gemm_nn: dict[tuple[int, int, int, bool], bool] = {}
+# hipBLASLt's default fp32 kernel for a given shape depends on the operand layout. Measured on the
+# device (a spin kernel holding the stream while ten calls per layout queue behind it, best of three
+# alternating trials), the transposed-weight ("NN") call is clearly faster only at 256 rows for the
+# two 768-wide-input projections: c_attn ([768] -> [2304]) 15.8 -> 12.8 us and c_fc (+ GELU,
+# [768] -> [3072]) 16.7 -> 13.7 us. At 224 or 320 rows, and for the [3072] -> [768] projection at
+# any row count, the weight as stored ("TN") is as fast or faster. The choice is this fixed table,
+# not a measurement at run time, so that every process computes every shape the same way (the two
+# layouts may round differently) and no live step pays for a probe.
+GEMM_NN_SHAPES: frozenset[tuple[int, int, int, bool]] = frozenset({
+    (256, 2304, 768, False),  # c_attn at the 256-row decode bucket
+    (256, 3072, 768, True),  # c_fc + GELU at the 256-row decode bucket
+})  # fmt: skip
 
 
 def _gemm(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, gelu: bool) -> torch.Tensor:
     if gelu:
         return torch._addmm_activation(bias, x, w, use_gelu=True)
     return torch.addmm(bias, x, w) if bias is not None else x @ w
-
-
-def _layout_times(x: torch.Tensor, weight: torch.Tensor, weight_t: torch.Tensor, bias, gelu: bool,
-                  trials: int = 3, calls: int = 10) -> tuple[float, float]:
-    """Device time (ms) of ``calls`` back-to-back GEMMs in the stored (TN) and transposed (NN) layouts,
-    the best of ``trials`` alternating trials. A spin kernel holds the stream while the calls are
-    queued behind it, so the events time the GEMMs themselves rather than the host's launch rate
-    (~20 us per call from Python, slower than these GEMMs run)."""
-    best = [math.inf, math.inf]
-    for _ in range(trials):
-        for i, w in enumerate((weight.t(), weight_t)):
-            _gemm(x, w, bias, gelu)
-            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            torch.cuda._sleep(2_000_000)
-            start.record()
-            for _ in range(calls):
-                _gemm(x, w, bias, gelu)
-            stop.record()
-            stop.synchronize()
-            best[i] = min(best[i], start.elapsed_time(stop))
-    return best[0], best[1]
-
-
-def _nn_is_faster(x: torch.Tensor, weight: torch.Tensor, weight_t: torch.Tensor, bias, gelu: bool) -> bool:
-    tn, nn = _layout_times(x, weight, weight_t, bias, gelu)
-    return nn < 0.95 * tn
 
 
 def transposed_weight(linear: torch.nn.Linear) -> torch.Tensor:
@@ -420,22 +399,19 @@ def transposed_weight(linear: torch.nn.Linear) -> torch.Tensor:
     return cached[1]
 
 
+def uses_nn_layout(rows: int, out_features: int, in_features: int, gelu: bool) -> bool:
+    """Whether ``linear`` runs this shape with the transposed weight copy (``GEMM_NN_SHAPES``)."""
+    return (rows, out_features, in_features, gelu) in GEMM_NN_SHAPES
+
+
 def linear(x: torch.Tensor, layer: torch.nn.Linear, gelu: bool = False) -> torch.Tensor:
-    """``x @ layer.weight.T + layer.bias`` (then the tanh GELU when ``gelu``) through hipBLASLt,
-    in whichever weight layout measured faster for this shape (see above). On the CPU: torch's
-    ``F.linear`` and the tanh GELU."""
+    """``x @ layer.weight.T + layer.bias`` (then the tanh GELU when ``gelu``) through hipBLASLt, in
+    the weight layout ``GEMM_NN_SHAPES`` names for this shape. On the CPU: torch's ``F.linear`` and
+    the tanh GELU."""
     if not x.is_cuda:
         y = torch.nn.functional.linear(x, layer.weight, layer.bias)
         return torch.nn.functional.gelu(y, approximate="tanh") if gelu else y
-    rows = x.shape[0]
     out_f, in_f = layer.weight.shape
-    key = (rows, out_f, in_f, gelu)
-    use_nn = _gemm_nn.get(key)
-    if use_nn is None:
-        use_nn = False
-        # Measured only for power-of-two row counts of at least 64 (the decode graph buckets),
-        # never while a graph is being captured; other shapes use the stored layout.
-        if rows >= 64 and rows & (rows - 1) == 0 and not torch.cuda.is_current_stream_capturing():
-            use_nn = _gemm_nn[key] = _nn_is_faster(x, layer.weight, transposed_weight(layer), layer.bias, gelu)
-    w = transposed_weight(layer) if use_nn else layer.weight.t()
+    nn_layout = uses_nn_layout(x.shape[0], out_f, in_f, gelu)
+    w = transposed_weight(layer) if nn_layout else layer.weight.t()
     return _gemm(x, w, layer.bias, gelu)

@@ -1,32 +1,40 @@
-"""FCFS continuous-batching scheduler (policies of tokquay/scheduler.py:1-31).
+"""Continuous-batching scheduler: which sequences run in the next step, and with how many tokens.
 
-* Alternating, prefill-priority steps: if a waiting request can be admitted the
-  step prefills only the newly admitted requests, otherwise it decodes every
-  running sequence.
-* FCFS admission with no skipping: admission stops at the first waiting request
-  that does not fit (sequence cap, padded-token budget, or blocks + watermark).
-* Preemption by recompute: when a decode step cannot grow some sequence's block
-  table, the newest running sequence is evicted and requeued at the front.
-* Up-front rejection of requests whose worst case can never fit.
-* Watermark: while others run, admission keeps ``watermark_blocks`` free.
+Policies are the reference's (tokquay/scheduler.py:1-31), because they decide
+which block tables the paged-attention kernels read and the reference's tests
+pin them:
 
-The scheduler grows block tables before the forward, which fixes the block
-tables the paged-attention kernels read.
+* first come, first served, and never past the head of the queue: admission
+  stops at the first waiting request that does not fit;
+* the default step kind alternates: a step that can admit someone prefills only
+  the newly admitted requests, any other step decodes every running sequence;
+* a step's budget counts padded tokens (rows x longest row);
+* when the pool cannot give a running sequence its next slot, the newest running
+  sequence is evicted, forgets its cache and goes back to the front of the queue
+  (recomputed later, prompt + output);
+* while others run, admission keeps ``watermark_blocks`` blocks free;
+* a request whose worst case can never fit is refused at ``add_request``.
 
-``chunked_prefill=True`` replaces the alternation with mixed steps (not in the
-reference, whose batches are padded): every running sequence that is decoding
-feeds its one token, and the remaining per-step budget - counted in real tokens,
-since the packed batch has no padding - goes to prefills in chunks of at most
-``prefill_chunk_tokens``: first the sequences already part-way through their
-prompt (oldest first), then new admissions (FCFS, same block and watermark
-rules). A prompt longer than the budget is then admissible: it is simply fed
-over several steps. Preemption is unchanged (newest first, recompute).
+How the decisions are organised here:
+
+* one admission routine for both step kinds (``_take_from_queue``): the caller
+  passes the token-budget test and how many tokens a new row feeds;
+* one growth routine (``_make_room``): every decoding sequence, oldest first,
+  gets its next slot, evicting from the newest end of ``running`` until it fits;
+* ``running`` is always in admission order, so "newest" is its last element.
+
+``chunked_prefill=True`` (not in the reference, whose rows are padded so it
+cannot mix) builds mixed steps: every decoding sequence feeds one token and the
+rest of the budget - real tokens, as the packed batch has no padding - goes to
+prompts in chunks of at most ``prefill_chunk_tokens``, sequences part-way
+through their prompt first (oldest first), then admissions from the queue.
 """
 
 from __future__ import annotations
 
 from collections import deque
 from dataclasses import dataclass, field
+from typing import Callable
 
 from tokquay_amd.kv_cache import BlockAllocator
 from tokquay_amd.sequence import Sequence, SequenceStatus
@@ -39,7 +47,8 @@ class RequestRejected(ValueError):
 @dataclass
 class SchedulerConfig:
     max_num_seqs: int = 64
-    # Per-step budget in padded tokens (batch size x longest row), as in the reference.
+    # Token budget per step: padded tokens (rows x longest row) in the alternating mode, real tokens
+    # in the chunked mode.
     max_num_batched_tokens: int = 2048
     max_model_len: int = 1024
     watermark_blocks: int = 1
@@ -62,10 +71,12 @@ class ScheduledBatch:
     padded_tokens: int = field(init=False)
 
     def __post_init__(self) -> None:
-        if self.new_lens is None:
-            self.padded_tokens = len(self.seqs) * max(s.num_uncached_tokens for s in self.seqs)
-        else:
+        # Fixed now: the sequences' uncached counts change once the step has run.
+        if self.new_lens is not None:
             self.padded_tokens = sum(self.new_lens)  # packed rows: nothing is padded
+        else:
+            widest = max(s.num_uncached_tokens for s in self.seqs)
+            self.padded_tokens = widest * len(self.seqs)
 
 
 class Scheduler:
@@ -73,165 +84,153 @@ class Scheduler:
         self.allocator = allocator
         self.config = config or SchedulerConfig()
         self.waiting: deque[Sequence] = deque()
-        self.running: list[Sequence] = []  # admission order; the last one is the newest
+        self.running: list[Sequence] = []  # admission order: running[-1] is the newest
         self.num_preemptions = 0
-        self.num_discarded_positions = 0
+        self.num_discarded_positions = 0  # cached positions thrown away by evictions
 
     # ---- requests ------------------------------------------------------------------
     def max_context(self, seq: Sequence) -> int:
-        """Most positions the sequence will ever cache (its last token never needs K/V)."""
-        return len(seq.prompt_token_ids) + seq.sampling.max_tokens - 1
+        """Positions the sequence can ever hold in the pool: the token sampled last is returned,
+        never fed, so it needs no K/V."""
+        return seq.sampling.max_tokens + len(seq.prompt_token_ids) - 1
 
     def rejection_reason(self, seq: Sequence) -> str | None:
-        ctx, cfg = self.max_context(seq), self.config
-        if ctx > cfg.max_model_len:
-            return f"prompt + max_tokens needs {ctx} positions but the model supports {cfg.max_model_len}"
+        """Why ``seq`` can never run here, or None. Checked in this order: model window, pool size,
+        then (alternating mode, where a recomputed sequence must be re-fed in one step) the budget."""
+        cfg, ctx = self.config, self.max_context(seq)
         blocks = self.allocator.blocks_needed(ctx)
-        if blocks > self.allocator.num_blocks:
-            return f"needs {blocks} KV blocks but the pool only has {self.allocator.num_blocks}"
-        if ctx > cfg.max_num_batched_tokens and not cfg.chunked_prefill:
-            return f"needs {ctx} tokens in one step but max_num_batched_tokens is {cfg.max_num_batched_tokens}"
-        return None
+        problems = (
+            (ctx > cfg.max_model_len,
+             f"prompt + max_tokens needs {ctx} positions but the model supports {cfg.max_model_len}"),
+            (blocks > self.allocator.num_blocks,
+             f"needs {blocks} KV blocks but the pool only has {self.allocator.num_blocks}"),
+            (not cfg.chunked_prefill and ctx > cfg.max_num_batched_tokens,
+             f"needs {ctx} tokens in one step but max_num_batched_tokens is {cfg.max_num_batched_tokens}"),
+        )  # fmt: skip
+        return next((msg for bad, msg in problems if bad), None)
 
     def add_request(self, seq: Sequence) -> None:
         reason = self.rejection_reason(seq)
-        if reason:
+        if reason is not None:
             raise RequestRejected(reason)
         seq.status = SequenceStatus.WAITING
         self.waiting.append(seq)
 
     def has_unfinished(self) -> bool:
-        return bool(self.waiting or self.running)
+        return len(self.waiting) + len(self.running) > 0
 
-    def finish(self, seq: Sequence, reason: str) -> None:
-        self.running.remove(seq)
-        self.allocator.free(seq)
+    def _retire(self, seq: Sequence, reason: str) -> None:
+        self.allocator.free(seq)  # a queued sequence holds no blocks: a no-op then
         seq.status = SequenceStatus.FINISHED
         seq.finish_reason = reason
 
+    def finish(self, seq: Sequence, reason: str) -> None:
+        self.running.remove(seq)
+        self._retire(seq, reason)
+
     def abort(self, seq: Sequence) -> None:
-        """Drop a request wherever it is; a no-op once it has finished."""
+        """Drop a request wherever it is (queued, requeued after an eviction, running); a no-op once
+        it has finished."""
         if seq.status is SequenceStatus.FINISHED:
             return
-        if seq in self.running:
-            self.running.remove(seq)
-        else:
-            self.waiting.remove(seq)
-        self.allocator.free(seq)
-        seq.status = SequenceStatus.FINISHED
-        seq.finish_reason = "abort"
+        (self.running if seq in self.running else self.waiting).remove(seq)
+        self._retire(seq, "abort")
+
+    # ---- building blocks -------------------------------------------------------------
+    def _evict_newest(self) -> Sequence:
+        victim = self.running.pop()
+        self.num_discarded_positions += victim.num_cached_tokens
+        self.allocator.free(victim)
+        victim.reset_for_recompute()  # status WAITING, no blocks, nothing cached; outputs kept
+        self.waiting.appendleft(victim)  # ahead of later arrivals: arrival order is kept
+        self.num_preemptions += 1
+        return victim
+
+    def _make_room(self, decoders: list[Sequence]) -> list[Sequence]:
+        """Give each sequence in ``decoders`` (oldest first) the slot its next token needs. When the
+        pool is short, evict from the newest end of ``running`` - possibly the sequence itself - until
+        it fits. Returns the evicted sequences in eviction order."""
+        alloc = self.allocator
+        evicted: list[Sequence] = []
+        for seq in decoders:
+            while seq.status is SequenceStatus.RUNNING and not alloc.can_append_slot(seq):
+                evicted.append(self._evict_newest())
+            if seq.status is SequenceStatus.RUNNING:
+                alloc.append_slot(seq)
+        return evicted
+
+    def _take_from_queue(self, fits_budget: Callable[[Sequence], bool], on_admit: Callable[[Sequence], None]) -> None:
+        """Admit queue heads while the sequence cap, ``fits_budget(head)`` and the free blocks (less
+        the watermark while anyone else holds blocks) allow; stop at the first head that does not fit.
+        An admitted sequence gets blocks for all its tokens and joins ``running``."""
+        cfg, alloc = self.config, self.allocator
+        while self.waiting and len(self.running) < cfg.max_num_seqs:
+            head = self.waiting[0]
+            if not fits_budget(head):
+                return
+            keep_free = cfg.watermark_blocks if self.running else 0
+            if alloc.num_free_blocks - keep_free < alloc.blocks_needed(head.num_tokens):
+                return
+            self.waiting.popleft()
+            alloc.allocate(head)
+            head.status = SequenceStatus.RUNNING
+            self.running.append(head)
+            on_admit(head)
 
     # ---- one decision --------------------------------------------------------------
     def schedule(self) -> ScheduledBatch | None:
         if self.config.chunked_prefill:
-            return self._schedule_chunked()
-        if self.waiting:
-            admitted = self._admit()
-            if admitted:
-                self.running.extend(admitted)
-                return ScheduledBatch(admitted, is_prefill=True)
+            return self._mixed_step()
+        admitted = self._prefill_admissions()
+        if admitted:
+            return ScheduledBatch(admitted, is_prefill=True)
         if not self.running:
             return None
-        return self._schedule_decode()
+        evicted = self._make_room(list(self.running))
+        # Only a lone sequence is ever evicted for its own sake, and then the whole pool is free for
+        # it (rejection guarantees it fits), so a decode batch is never empty.
+        assert self.running, "scheduler evicted every running sequence"
+        return ScheduledBatch(list(self.running), is_prefill=False, preempted=evicted)
 
-    def _admit(self) -> list[Sequence]:
-        cfg, alloc = self.config, self.allocator
+    def _prefill_admissions(self) -> list[Sequence]:
+        """Alternating mode: the requests a prefill-only step admits (all their uncached tokens:
+        prompt, plus outputs after an eviction), within the padded-token budget."""
         admitted: list[Sequence] = []
-        longest = 0
-        while self.waiting and len(self.running) + len(admitted) < cfg.max_num_seqs:
-            seq = self.waiting[0]
-            n = seq.num_tokens  # all uncached: prompt (+ output when recomputing)
-            if (len(admitted) + 1) * max(longest, n) > cfg.max_num_batched_tokens:
-                break
-            reserve = cfg.watermark_blocks if (self.running or admitted) else 0
-            if alloc.blocks_needed(n) + reserve > alloc.num_free_blocks:
-                break  # never skip the head of the queue
-            self.waiting.popleft()
-            alloc.allocate(seq)
-            seq.status = SequenceStatus.RUNNING
-            longest = max(longest, n)
-            admitted.append(seq)
+        widest = [0]
+
+        def fits(head: Sequence) -> bool:
+            width = max(widest[0], head.num_tokens)
+            return width * (len(admitted) + 1) <= self.config.max_num_batched_tokens
+
+        def admit(head: Sequence) -> None:
+            widest[0] = max(widest[0], head.num_tokens)
+            admitted.append(head)
+
+        self._take_from_queue(fits, admit)
         return admitted
 
-    def _schedule_decode(self) -> ScheduledBatch:
-        alloc, running = self.allocator, self.running
-        preempted: list[Sequence] = []
-        i = 0
-        while i < len(running):
-            seq = running[i]
-            evicted_self = False
-            while not alloc.can_append_slot(seq):
-                victim = running.pop()  # newest; may be `seq` itself
-                self._preempt(victim)
-                preempted.append(victim)
-                if victim is seq:
-                    evicted_self = True
-                    break
-            if not evicted_self:
-                alloc.append_slot(seq)
-                i += 1
-        # The oldest sequence is only evicted when alone, and then the whole pool is free
-        # for it (rejection guarantees it fits), so the batch cannot be empty.
-        assert running, "scheduler evicted every running sequence"
-        return ScheduledBatch(list(running), is_prefill=False, preempted=preempted)
+    def _mixed_step(self) -> ScheduledBatch | None:
+        """Chunked mode: every decoding sequence's token, then prompt chunks in the remaining budget."""
+        cfg = self.config
+        decoders = [s for s in self.running if s.num_cached_tokens > 0 and s.num_uncached_tokens == 1]
+        evicted = self._make_room(decoders)
+        feeds: dict[int, int] = {id(s): 1 for s in decoders if s.status is SequenceStatus.RUNNING}
+        num_decoding = len(feeds)
+        room = [cfg.max_num_batched_tokens - num_decoding]
 
-    def _grow_decoders(self, decoders: list[Sequence]) -> list[Sequence]:
-        """Make room for each decoding sequence's next token, evicting the newest running sequences
-        (decoding or part-way through their prompt) when the pool is exhausted."""
-        alloc, running = self.allocator, self.running
-        preempted: list[Sequence] = []
-        for seq in decoders:
-            if seq not in running:
-                continue  # evicted while making room for an older one
-            while not alloc.can_append_slot(seq):
-                victim = running.pop()
-                self._preempt(victim)
-                preempted.append(victim)
-                if victim is seq:
-                    break
-            else:
-                alloc.append_slot(seq)
-        return preempted
+        def chunk(seq: Sequence) -> None:
+            n = min(seq.num_uncached_tokens, cfg.prefill_chunk_tokens, room[0])
+            feeds[id(seq)] = n
+            room[0] -= n
 
-    def _schedule_chunked(self) -> ScheduledBatch | None:
-        cfg, alloc = self.config, self.allocator
-        decoders = [s for s in self.running if s.num_uncached_tokens == 1 and s.num_cached_tokens > 0]
-        preempted = self._grow_decoders(decoders)
-        decoders = [s for s in decoders if s in self.running]
-        budget = cfg.max_num_batched_tokens - len(decoders)
-        chunks: list[tuple[Sequence, int]] = []
-        # Sequences part-way through their prompt (or recompute), oldest first.
-        for seq in self.running:
-            if budget <= 0:
+        for seq in list(self.running):  # prompts already part-way through, oldest first
+            if room[0] <= 0:
                 break
-            if seq in decoders:
-                continue
-            n = min(seq.num_uncached_tokens, cfg.prefill_chunk_tokens, budget)
-            chunks.append((seq, n))
-            budget -= n
-        # New admissions, FCFS: blocks for the whole prompt are taken at admission.
-        while self.waiting and budget > 0 and len(self.running) < cfg.max_num_seqs:
-            seq = self.waiting[0]
-            reserve = cfg.watermark_blocks if self.running else 0
-            if alloc.blocks_needed(seq.num_tokens) + reserve > alloc.num_free_blocks:
-                break
-            self.waiting.popleft()
-            alloc.allocate(seq)
-            seq.status = SequenceStatus.RUNNING
-            self.running.append(seq)
-            n = min(seq.num_uncached_tokens, cfg.prefill_chunk_tokens, budget)
-            chunks.append((seq, n))
-            budget -= n
-        if not decoders and not chunks:
+            if id(seq) not in feeds:
+                chunk(seq)
+        self._take_from_queue(lambda head: room[0] > 0, chunk)
+        if not feeds:
             return None
-        order = {id(s): i for i, s in enumerate(self.running)}  # keep admission order in the batch
-        rows = sorted([(s, 1) for s in decoders] + chunks, key=lambda sn: order[id(sn[0])])
-        return ScheduledBatch([s for s, _ in rows], is_prefill=bool(chunks), preempted=preempted,
-                              new_lens=[n for _, n in rows])  # fmt: skip
-
-    def _preempt(self, seq: Sequence) -> None:
-        self.num_discarded_positions += seq.num_cached_tokens
-        self.allocator.free(seq)
-        seq.reset_for_recompute()
-        self.waiting.appendleft(seq)
-        self.num_preemptions += 1
+        rows = [s for s in self.running if id(s) in feeds]  # admission order
+        return ScheduledBatch(rows, is_prefill=len(feeds) > num_decoding, preempted=evicted,
+                              new_lens=[feeds[id(s)] for s in rows])  # fmt: skip
