@@ -296,8 +296,9 @@ def mixed_engine(chunked: bool, seed: int = 5) -> dict:
     prompts of U[512,1024] tokens arrive. With chunked prefill the prompts are fed 256 tokens per
     step next to the decode rows; with the reference's alternating policy (2,048 padded tokens per
     step) the prompts are prefilled in steps of their own while the decode rows wait. Reports the
-    steps and wall time until every prompt has its first token, and the longest gap a decoding
-    sequence saw between two tokens meanwhile."""
+    steps and wall time from the prompts' arrival until every prompt has its first token, and the
+    longest wait a decoding sequence saw for a token from the prompts' arrival until each decoding
+    sequence has had a token after the last prompt's first."""
     import torch
 
     from tokquay_amd.engine import Engine
@@ -322,23 +323,26 @@ def mixed_engine(chunked: bool, seed: int = 5) -> dict:
     long_ids = {engine.add_request(p, SamplingParams(max_tokens=1, ignore_eos=True)).seq_id for p in prompts}
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    last: dict[int, float | None] = {i: None for i in decoders}
-    worst_gap, steps, pending = 0.0, 0, set(long_ids)
-    while pending:
+    last: dict[int, float] = {i: t0 for i in decoders}  # the stall counts from the prompts' arrival
+    worst_gap, steps, pending, prompts_done_s = 0.0, 0, set(long_ids), None
+    after: set[int] = set()  # decoders that emitted after the last prompt's first token
+    while (pending or after != decoders) and steps < 1000:
         events = engine.step()
         now = time.perf_counter()
         steps += 1
         for ev in events:
             pending.discard(ev.seq_id)
             if ev.seq_id in last:
-                if last[ev.seq_id] is not None:
-                    worst_gap = max(worst_gap, now - last[ev.seq_id])
+                worst_gap = max(worst_gap, now - last[ev.seq_id])
                 last[ev.seq_id] = now
-    elapsed = time.perf_counter() - t0
+                if prompts_done_s is not None:
+                    after.add(ev.seq_id)
+        if not pending and prompts_done_s is None:
+            prompts_done_s, done_steps = now - t0, steps
     engine.drain()
     engine.allocator.check_device_errors()
     return {"policy": "chunked prefill (256-token chunks)" if chunked else "alternating (reference)",
-            "steps_until_prompts_done": steps, "ms_until_prompts_done": round(elapsed * 1e3, 2),
+            "steps_until_prompts_done": done_steps, "ms_until_prompts_done": round(prompts_done_s * 1e3, 2),
             "max_decode_gap_ms": round(worst_gap * 1e3, 2)}  # fmt: skip
 
 
