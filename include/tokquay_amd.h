@@ -7,6 +7,7 @@
  *   tq_cache_write    scatter each new token's K/V rows into the block pool
  *   tq_paged_decode   one-query-per-sequence attention straight off the pool
  *   tq_paged_decode_write  the same, with the new token's cache write folded in
+ *                     (tq_paged_decode_write_static: without a workspace argument)
  *   tq_paged_prefill  causal (chunked) prefill attention straight off the pool
  *
  * plus two kernels of the model step around them:
@@ -178,6 +179,38 @@ tq_status tq_paged_decode_write(float* out, int64_t out_row_stride,
 /* Bytes of workspace tq_paged_decode needs for these sizes (0 if none). */
 size_t tq_paged_decode_workspace_size(int32_t num_seqs, int32_t num_heads, int32_t head_dim,
                                       int32_t max_context_len, int32_t partition_tokens);
+
+/* Bytes of the per-GPU device array tq_paged_decode_write_static keeps its partials in. */
+#define TQ_STATIC_SCRATCH_BYTES (8u << 20)
+
+/*
+ * tq_paged_decode_write without the workspace arguments: it allocates nothing and takes no
+ * caller memory beyond its inputs and outputs. Same semantics, kernels and bits as
+ * tq_paged_decode_write. When tq_paged_decode_workspace_size(num_seqs, num_heads, head_dim,
+ * max_context_len, partition_tokens) is not 0 (explicit partitions that split sequences) the
+ * partition partials go to a static device array of TQ_STATIC_SCRATCH_BYTES (8 MiB) per GPU,
+ * held until the process ends; a call that would need more returns TQ_ERR_WORKSPACE before any
+ * launch. The array's device address is looked up on the first call that needs it on each
+ * device (hipGetSymbolAddress, with that device current); `stream` must belong to the current
+ * device (else TQ_ERR_INVALID_ARGUMENT). Every call on one GPU shares that GPU's array and it
+ * keeps the last call's contents: calls that overlap on one GPU (on different streams) race;
+ * order them on one stream.
+ *
+ * No counterpart in the reference (it has no kernels). For callers that cannot allocate device
+ * memory: code under HIP graph capture, serving loops and harnesses that forbid allocation.
+ */
+tq_status tq_paged_decode_write_static(float* out, int64_t out_row_stride,
+                                       const float* q, int64_t q_row_stride,
+                                       const float* k_new, int64_t k_new_row_stride,
+                                       const float* v_new, int64_t v_new_row_stride,
+                                       float* pool, int64_t num_blocks, int32_t num_layers,
+                                       int32_t num_heads, int32_t block_size, int32_t head_dim, int32_t layer,
+                                       const int32_t* block_tables, int64_t block_table_stride,
+                                       int32_t max_blocks_per_seq,
+                                       const int32_t* context_lens, const int32_t* seq_order,
+                                       int32_t num_seqs, int32_t max_context_len,
+                                       float scale, int32_t partition_tokens,
+                                       int32_t* d_error, void* stream);
 
 /*
  * Paged prefill / chunked-prefill attention. Sequence b feeds

@@ -15,6 +15,7 @@ c_i32p = ctypes.c_void_p
 c_i64p = ctypes.c_void_p
 
 TQ_OK = 0
+STATIC_SCRATCH_BYTES = 8 << 20  # TQ_STATIC_SCRATCH_BYTES: tq_paged_decode_write_static's per-GPU array
 STATUS_NAMES = {0: "ok", 1: "invalid argument", 2: "unsupported shape", 3: "workspace missing or too small", 4: "HIP runtime error"}
 
 # Bits kernels OR into the optional device error word.
@@ -67,6 +68,21 @@ SIGNATURES: dict[str, tuple] = {
             c_i32p, c_i32p, ctypes.c_int32, ctypes.c_int32,  # context_lens, seq_order, num_seqs, max_context_len
             ctypes.c_float, ctypes.c_int32,  # scale, partition_tokens
             ctypes.c_void_p, ctypes.c_size_t,  # workspace, workspace_bytes
+            c_i32p, ctypes.c_void_p,  # d_error, stream
+        ],
+    ),
+    "tq_paged_decode_write_static": (
+        ctypes.c_int,
+        [
+            c_f32p, ctypes.c_int64,  # out, out_row_stride
+            c_f32p, ctypes.c_int64,  # q, q_row_stride
+            c_f32p, ctypes.c_int64,  # k_new, k_new_row_stride
+            c_f32p, ctypes.c_int64,  # v_new, v_new_row_stride
+            c_f32p, ctypes.c_int64, ctypes.c_int32,  # pool, num_blocks, num_layers
+            ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,  # num_heads, block_size, head_dim, layer
+            c_i32p, ctypes.c_int64, ctypes.c_int32,  # block_tables, block_table_stride, max_blocks_per_seq
+            c_i32p, c_i32p, ctypes.c_int32, ctypes.c_int32,  # context_lens, seq_order, num_seqs, max_context_len
+            ctypes.c_float, ctypes.c_int32,  # scale, partition_tokens
             c_i32p, ctypes.c_void_p,  # d_error, stream
         ],
     ),

@@ -34,7 +34,15 @@
 #include <hip/hip_ext.h>
 #include <math.h>
 
+#include <mutex>
+
 #include "tq_internal.h"
+
+// Partition partials of tq_paged_decode_write_static: the same [num_seqs][num_heads][parts][68]
+// layout the caller-supplied workspace of the other entry points holds. One copy per GPU, held
+// until the process ends; host code reaches it only through the address hipGetSymbolAddress
+// gives on that device (the array's name in host code is a host-side stand-in).
+static __device__ __align__(256) float scratch[TQ_STATIC_SCRATCH_BYTES / sizeof(float)];
 
 namespace tq {
 namespace {
@@ -736,3 +744,73 @@ extern "C" tq_status tq_paged_decode_write(float* out, int64_t out_row_stride, c
                            partition_tokens, workspace, workspace_bytes, d_error, stream);
 }
 
+
+namespace tq {
+namespace {
+
+constexpr int kMaxStaticDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_address[kMaxStaticDevices] = {};
+
+// The device address of `scratch` on the current device: looked up with hipGetSymbolAddress the
+// first time the current device asks, with that device current, then kept per device. `stream`
+// must belong to the current device (a stream of another GPU would be handed this GPU's array).
+tq_status static_scratch(void* stream, void** address) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return record_hip_error(e);
+  if (dev < 0 || dev >= kMaxStaticDevices) return TQ_ERR_UNSUPPORTED;
+  if (stream != nullptr) {
+    hipDevice_t stream_dev = -1;
+    e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &stream_dev);
+    if (e != hipSuccess) return record_hip_error(e);
+    if (stream_dev != dev) return TQ_ERR_INVALID_ARGUMENT;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_address[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return record_hip_error(e);
+    if (p == nullptr) return TQ_ERR_HIP;
+    g_scratch_address[dev] = p;
+  }
+  *address = g_scratch_address[dev];
+  return TQ_OK;
+}
+
+}  // namespace
+}  // namespace tq
+
+extern "C" tq_status tq_paged_decode_write_static(float* out, int64_t out_row_stride, const float* q,
+                                                  int64_t q_row_stride, const float* k_new,
+                                                  int64_t k_new_row_stride, const float* v_new,
+                                                  int64_t v_new_row_stride, float* pool, int64_t num_blocks,
+                                                  int32_t num_layers, int32_t num_heads, int32_t block_size,
+                                                  int32_t head_dim, int32_t layer, const int32_t* block_tables,
+                                                  int64_t block_table_stride, int32_t max_blocks_per_seq,
+                                                  const int32_t* context_lens, const int32_t* seq_order,
+                                                  int32_t num_seqs, int32_t max_context_len, float scale,
+                                                  int32_t partition_tokens, int32_t* d_error, void* stream) {
+  using namespace tq;
+  // The partials are written by the partition kernel before the merge kernel reads them, for
+  // exactly the partitions each sequence has, so nothing in the array needs to start at zero.
+  const size_t need = tq_paged_decode_workspace_size(num_seqs, num_heads, head_dim, max_context_len,
+                                                     partition_tokens);
+  if (need > TQ_STATIC_SCRATCH_BYTES) {
+    take_timing_events();  // armed events apply to this call only
+    return TQ_ERR_WORKSPACE;
+  }
+  void* ws = nullptr;
+  if (need > 0) {
+    const tq_status st = static_scratch(stream, &ws);
+    if (st != TQ_OK) {
+      take_timing_events();
+      return st;
+    }
+  }
+  return tq_paged_decode_write(out, out_row_stride, q, q_row_stride, k_new, k_new_row_stride, v_new,
+                               v_new_row_stride, pool, num_blocks, num_layers, num_heads, block_size, head_dim,
+                               layer, block_tables, block_table_stride, max_blocks_per_seq, context_lens,
+                               seq_order, num_seqs, max_context_len, scale, partition_tokens, ws,
+                               need > 0 ? (size_t)TQ_STATIC_SCRATCH_BYTES : 0, d_error, stream);
+}
