@@ -16,6 +16,8 @@
  *   tq_add_layernorm  residual add fused with the LayerNorm that follows it
  *   tq_skinny_linear  linear layer of at most 64 rows, LayerNorm / bias / GELU /
  *                     residual add fused in (small-batch decode steps)
+ *   tq_skinny_linear_argmax  the LM head of at most 16 rows with the greedy argmax
+ *                     fused in: only ids are written
  *   tq_embed_rows     token + position embeddings of each row
  *
  * KV pool layout (identical to the reference's, bit for bit):
@@ -303,6 +305,29 @@ tq_status tq_skinny_linear(float* y, int64_t y_stride, const float* x, int64_t x
                            const float* w, const float* bias, int32_t N, int32_t K, const float* ln_gamma,
                            const float* ln_beta, float ln_eps, int32_t epilogue, void* workspace,
                            size_t workspace_bytes, void* stream);
+
+/*
+ * Greedy ids of a linear layer of at most 16 rows, with no logits written:
+ *
+ *   h = LN(x) if ln_gamma else x;   ids[m] = the lowest n < N with (h[m] W^T + bias)[n] maximal
+ *
+ * in the order of tq_argmax_rows (NaN above every number, the first NaN wins; -0 ties +0).
+ * ids is int64[M]. x [M, 768] (row stride x_stride), W [N, 768] contiguous, bias may be NULL;
+ * M <= 16, N < 2^31 - 32; alignment as tq_skinny_linear. Each 32-column slice of the logits is
+ * reduced on chip to one candidate per row, kept in the workspace; a second kernel of the same
+ * call reduces the candidates of each row. The workspace, of
+ * tq_skinny_linear_argmax_workspace_size(N) bytes (16-byte aligned), needs no initialisation;
+ * calls sharing a workspace must not run concurrently.
+ *
+ * Replaces, for decode steps of at most 16 greedy sequences, the tied LM head with ln_f in front
+ * (tokquay/model.py:180-181, W = wte, no bias) together with the batched argmax of
+ * Engine._sample (tokquay/engine.py:190): only the [M] ids are written.
+ */
+size_t tq_skinny_linear_argmax_workspace_size(int32_t N);
+tq_status tq_skinny_linear_argmax(int64_t* ids, const float* x, int64_t x_stride, int32_t M, const float* w,
+                                  const float* bias, int32_t N, int32_t K, const float* ln_gamma,
+                                  const float* ln_beta, float ln_eps, void* workspace, size_t workspace_bytes,
+                                  void* stream);
 
 /*
  * x[r] = wte[id_r] + wpe[positions[r]] for rows r < rows, C columns (a multiple

@@ -73,7 +73,8 @@ def test_graph_replays_match_eager_steps(model):
                 s.append_token(t)
                 alloc.append_slot(s)
     ga.check_device_errors()
-    assert set(graphs.graphs) == {8, 4}  # 7 sequences -> bucket 8, then 3 -> bucket 4, each captured once
+    # 7 sequences -> bucket 8, then 3 -> bucket 4, each captured once (logits graphs: forward() wants them)
+    assert set(graphs.graphs) == {(8, False), (4, False)}
     for s_g, s_e in zip(gseqs, eseqs):
         assert s_g.num_cached_tokens == s_e.num_cached_tokens
     # Identical pools: the replayed cache writes landed in the same slots with the same bits... up to

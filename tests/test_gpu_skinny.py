@@ -156,3 +156,99 @@ def test_results_are_deterministic(N, K, M):
     for _ in range(20):
         assert torch.equal(ops.skinny_linear(x, w, b), first)
     torch.testing.assert_close(first.cpu(), F.linear(x.cpu(), w.cpu(), b.cpu()), **TOL)
+
+
+# ---- the LM head with the greedy argmax fused in (tq_skinny_linear_argmax) ----------------------
+def _lm_head_case(M: int, seed: int):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, 768, generator=g) * 2 + 0.3
+    w = torch.randn(50257, 768, generator=g) * 0.02
+    gamma, beta = torch.randn(768, generator=g) * 0.5 + 1, torch.randn(768, generator=g) * 0.1
+    return x, w, gamma, beta
+
+
+@pytest.mark.parametrize("M", [1, 2, 5, 8, 13, 16])
+def test_lm_head_argmax_equals_logits_then_argmax(M):
+    """Fused ids == tq_argmax_rows over the unfused kernel's logits (the same products summed in the
+    same order, so the same bits), and == a float64 CPU argmax wherever its top-1 / top-2 gap is not a
+    near tie."""
+    x, w, gamma, beta = _lm_head_case(M, M)
+    ln = (gamma.cuda(), beta.cuda(), 1e-5)
+    xc, wc = x.cuda(), w.cuda()
+    got = ops.skinny_linear_argmax(xc, wc, None, ln=ln)
+    logits = ops.skinny_linear(xc, wc, None, ln=ln)
+    assert torch.equal(got, ops.argmax_rows(logits))
+    ref = F.linear(F.layer_norm(x.double(), (768,), gamma.double(), beta.double(), 1e-5), w.double())
+    top2 = ref.topk(2, dim=-1)
+    gap = top2.values[:, 0] - top2.values[:, 1]
+    for m in range(M):
+        assert int(got[m]) == int(top2.indices[m, 0]) or float(gap[m]) < 1e-4, (m, float(gap[m]))
+    # Without the LayerNorm and with a bias.
+    b = torch.randn(50257, generator=torch.Generator().manual_seed(3)) * 0.1
+    got = ops.skinny_linear_argmax(xc, wc, b.cuda())
+    assert torch.equal(got, ops.argmax_rows(ops.skinny_linear(xc, wc, b.cuda())))
+
+
+def test_lm_head_argmax_ties_nans_and_workspace_reuse():
+    """Ties keep the lowest column, inside one 32-column slice and across slices; a NaN logit wins
+    and the first NaN column is taken; calls of different sizes in a row, sharing the workspace
+    (the previous call's candidates still in it), are each correct."""
+    x, w, gamma, beta = _lm_head_case(3, 99)
+    h = F.layer_norm(x, (768,), gamma, beta, 1e-5)
+    # Row 0: columns 40000 and 100 (different slices) tie above everything else.
+    # Row 1: columns 7 and 5 (one slice) tie above everything else.
+    w[100] = w[40000] = h[0] / h[0].norm() * 5
+    w[5] = w[7] = h[1] / h[1].norm() * 5
+    x[2] = float("nan")  # row 2: every logit is NaN, the first column wins
+    ln = (gamma.cuda(), beta.cuda(), 1e-5)
+    got = ops.skinny_linear_argmax(x.cuda(), w.cuda(), None, ln=ln).tolist()
+    assert got == [100, 5, 0]
+    ref = F.linear(F.layer_norm(x, (768,), gamma, beta, 1e-5), w)
+    assert got == ref.argmax(-1).tolist()  # torch's rule agrees
+    # One NaN column: it wins in every row (torch's argmax does the same).
+    xn, wn, gn, bn = _lm_head_case(2, 7)
+    wn[777, 0] = float("nan")
+    lnn = (gn.cuda(), bn.cuda(), 1e-5)
+    got_nan = ops.skinny_linear_argmax(xn.cuda(), wn.cuda(), None, ln=lnn).tolist()
+    assert got_nan == [777, 777] == F.linear(F.layer_norm(xn, (768,), gn, bn, 1e-5), wn).argmax(-1).tolist()
+    # Calls of other sizes right after, then the first again: each is correct and repeatable.
+    for M, seed in ((16, 5), (1, 6)):
+        x2, w2, g2, b2 = _lm_head_case(M, seed)
+        ln2 = (g2.cuda(), b2.cuda(), 1e-5)
+        ids = ops.skinny_linear_argmax(x2.cuda(), w2.cuda(), None, ln=ln2)
+        assert torch.equal(ids, ops.argmax_rows(ops.skinny_linear(x2.cuda(), w2.cuda(), None, ln=ln2)))
+    assert ops.skinny_linear_argmax(x.cuda(), w.cuda(), None, ln=ln).tolist() == got
+    with pytest.raises(ValueError):
+        ops.skinny_linear_argmax(torch.zeros(17, 768, device="cuda"), w.cuda())
+
+
+@pytest.mark.parametrize("n", [1, 3, 8, 16])
+def test_ids_only_graph_matches_logits_graph(model, n):
+    """The ids-only decode graph (fused head + argmax, no logits) emits the same ids as the graph
+    that writes logits and runs tq_argmax_rows, step after step."""
+    rng = random.Random(100 + n)
+    prompts = [[rng.randrange(50256) for _ in range(rng.randint(3, 90))] for _ in range(n)]
+    states = []
+    for _ in range(2):
+        alloc = BlockAllocator(model.cfg, 8 * n + 64, 16, device="cuda")
+        seqs = [Sequence(i, list(p)) for i, p in enumerate(prompts)]
+        for s in seqs:
+            alloc.allocate(s)
+        first = paged_forward(model, alloc, seqs).argmax(-1).tolist()
+        for s, t in zip(seqs, first):
+            s.append_token(t)
+            alloc.append_slot(s)
+        states.append((alloc, seqs, DecodeGraphs(model, alloc, max_batch=16)))
+    for _ in range(5):
+        outs = []
+        for i, (alloc, seqs, graphs) in enumerate(states):
+            logits, ids = graphs.launch(seqs, logits=(i == 1))
+            assert (logits is None) == (i == 0)
+            outs.append(ids.tolist())
+        assert outs[0] == outs[1]
+        for alloc, seqs, _ in states:
+            for s, t in zip(seqs, outs[1]):
+                s.append_token(t)
+                alloc.append_slot(s)
+    for alloc, _, _ in states:
+        alloc.check_device_errors()

@@ -65,7 +65,8 @@ class ToyGraphs:
         self.rows: list[tuple[object, int]] = []  # (sequence, fed position) of every launched row
         self.src_launches = 0
 
-    def launch(self, seqs, src_rows=None):
+    def launch(self, seqs, src_rows=None, logits=True):
+        """Like DecodeGraphs.launch: ``logits=False`` returns only the ids (the fused-head graph)."""
         prev = self.tokens.clone()
         out = []
         for i, s in enumerate(seqs):
@@ -83,7 +84,7 @@ class ToyGraphs:
             s.num_cached_tokens += 1
         self.src_launches += src_rows is not None
         self.tokens[: len(seqs)] = torch.tensor(out, dtype=torch.int64)
-        return one_hot(out), self.tokens[: len(seqs)]
+        return (one_hot(out) if logits else None), self.tokens[: len(seqs)]
 
 
 class ToyEngine(Engine):

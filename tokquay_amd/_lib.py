@@ -120,6 +120,16 @@ SIGNATURES: dict[str, tuple] = {
             ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,  # workspace, workspace_bytes, stream
         ],
     ),
+    "tq_skinny_linear_argmax": (
+        ctypes.c_int,
+        [
+            c_i64p, c_f32p, ctypes.c_int64, ctypes.c_int32,  # ids, x, x_stride, M
+            c_f32p, c_f32p, ctypes.c_int32, ctypes.c_int32,  # w, bias, N, K
+            c_f32p, c_f32p, ctypes.c_float,  # ln_gamma, ln_beta, ln_eps
+            ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,  # workspace, workspace_bytes, stream
+        ],
+    ),
+    "tq_skinny_linear_argmax_workspace_size": (ctypes.c_size_t, [ctypes.c_int32]),
     "tq_skinny_linear_workspace_size": (ctypes.c_size_t, [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]),
     "tq_embed_rows": (
         ctypes.c_int,

@@ -2,11 +2,7 @@
 //
 // One 1024-thread workgroup per row. Every candidate is folded into a 64-bit
 // key whose unsigned order is the order the reference's batched argmax uses
-// (torch's argmax over the last dimension):
-//
-//   high 32 bits: the float mapped to an unsigned integer of the same order
-//                 (-0 folded onto +0, so they tie; NaN above +inf);
-//   low 32 bits:  0xFFFFFFFF - column, so equal values keep the lowest column.
+// (torch's argmax over the last dimension; argmax_key in tq_internal.h).
 //
 // A plain unsigned max over keys then is the argmax, with no comparator
 // branches: per-thread max over a strided sweep (8 loads in flight per thread),
@@ -24,25 +20,10 @@ namespace {
 constexpr int kArgmaxThreads = 1024;
 constexpr int kArgmaxUnroll = 8;
 
-__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t col) {
-  uint32_t u;
-  if (v != v) {
-    u = 0xFFFFFFFFu;  // every NaN ranks above every number; the first NaN wins
-  } else {
-    u = __float_as_uint(v == 0.0f ? 0.0f : v);
-    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  }
-  return ((uint64_t)u << 32) | (uint64_t)(0xFFFFFFFFu - col);
-}
-
-__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
-
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(int64_t* out, const float* logits,
                                                                      int64_t row_stride, int32_t cols) {
   const float* p = logits + (int64_t)blockIdx.x * row_stride;
-  // Key 0 is below every real key: the smallest float key is -inf's, 0x007FFFFF in the
-  // high half, and columns stay below 0xFFFFFFFF.
-  uint64_t best = 0;
+  uint64_t best = 0;  // no candidate yet
   int i = threadIdx.x;
   constexpr int kSpan = kArgmaxThreads * kArgmaxUnroll;
   for (; i + (kArgmaxUnroll - 1) * kArgmaxThreads < cols; i += kSpan) {
@@ -66,7 +47,7 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(int64_t* ou
     best = lane < kArgmaxThreads / kWave ? s_best[lane] : 0;
 #pragma unroll
     for (int off = kArgmaxThreads / kWave / 2; off > 0; off >>= 1) best = max_u64(best, __shfl_xor(best, off));
-    if (lane == 0) out[blockIdx.x] = (int64_t)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFu));
+    if (lane == 0) out[blockIdx.x] = argmax_key_column(best);
   }
 }
 

@@ -75,4 +75,28 @@ __device__ __forceinline__ void flag_error(int32_t* d_error, int bits) {
   if (d_error != nullptr) atomicOr(d_error, bits);
 }
 
+// Greedy-sampling key of logit v in column col: its unsigned order is the order of the
+// reference's batched argmax (torch's argmax over the last dimension).
+//   high 32 bits: the float mapped to an unsigned integer of the same order (-0 folded onto
+//                 +0, so they tie; every NaN above +inf, so the first NaN wins);
+//   low 32 bits:  0xFFFFFFFF - col, so equal values keep the lowest column.
+// Key 0 is below every real key (the smallest float key is -inf's, 0x007FFFFF in the high
+// half, and columns stay below 0xFFFFFFFF): it stands for "no candidate".
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t col) {
+  uint32_t u;
+  if (v != v) {
+    u = 0xFFFFFFFFu;
+  } else {
+    u = __float_as_uint(v == 0.0f ? 0.0f : v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  }
+  return ((uint64_t)u << 32) | (uint64_t)(0xFFFFFFFFu - col);
+}
+
+__device__ __forceinline__ int64_t argmax_key_column(uint64_t key) {
+  return (int64_t)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFu));
+}
+
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
 }  // namespace tq

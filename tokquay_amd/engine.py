@@ -200,15 +200,20 @@ class Engine:
         """One step, synchronously: forward, sample, append, stop checks."""
         greedy = None
         if self.graphs is not None and not batch.is_prefill:
-            logits, greedy = self.graphs.launch(batch.seqs)
+            # All-greedy steps need only ids: small buckets then never write logits.
+            want_logits = any(s.sampling.temperature > 0 for s in batch.seqs)
+            logits, greedy = self.graphs.launch(batch.seqs, logits=want_logits)
         else:
             logits = self._eager_forward(batch.seqs, batch.new_lens)
         self.last_step = StepInfo(batch.is_prefill, len(batch.seqs), batch.padded_tokens, self.kv_snapshot())
         # A sequence samples once all its tokens are cached; a chunked prompt part-way through does not.
         done = [i for i, s in enumerate(batch.seqs) if s.num_cached_tokens == s.num_tokens]
         if len(done) < len(batch.seqs):
-            logits = logits[done]
-            greedy = None
+            if logits is None:  # ids-only decode step (every row is done after a decode step anyway)
+                greedy = greedy[torch.tensor(done, device=greedy.device)]
+            else:
+                logits = logits[done]
+                greedy = None
         seqs = [batch.seqs[i] for i in done]
         tokens = self._sample(seqs, logits, greedy) if seqs else []
         return self._emit(seqs, tokens)
@@ -233,7 +238,7 @@ class Engine:
 
     def _launch(self, seqs: list[Sequence], src_rows: list[int] | None, padded: int) -> _InFlight:
         """Enqueue one graph decode step and the copy of its greedy ids to the host."""
-        _, ids = self.graphs.launch(seqs, src_rows)
+        _, ids = self.graphs.launch(seqs, src_rows, logits=False)
         if self._host_ids is None:
             cap = self.graphs.capacity
             self._host_ids = [torch.empty(cap, dtype=torch.int64, pin_memory=ids.is_cuda) for _ in range(2)]

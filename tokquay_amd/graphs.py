@@ -9,7 +9,9 @@ rows run the fused small-batch path (``GPT2.skinny_logits``: each linear of a
 block with its LayerNorm / GELU / residual add in one ``tq_skinny_linear`` launch,
 about 65 launches per step; the LM head fused with ``ln_f`` up to 16 rows, else
 ``ln_f`` alone and the head on hipBLASLt); larger buckets the library GEMMs with
-``tq_add_layernorm``.
+``tq_add_layernorm``. A step whose rows are all greedy at most 16 rows replays an
+ids-only graph instead: the LM head with ``ln_f`` and the argmax in one
+``tq_skinny_linear_argmax`` launch, no logits written.
 
 What changes between steps lives in static device buffers at fixed addresses,
 refreshed by one host-to-device copy per step: token ids, positions,
@@ -146,12 +148,21 @@ class DecodeGraphs:
     def capacity(self) -> int:
         return self.static.capacity
 
-    def _forward(self, rows: int) -> torch.Tensor:
+    def fused_greedy(self, rows: int) -> bool:
+        """Whether a bucket's ids-only graph runs the LM head with the argmax fused in (no logits):
+        the small-batch path with the head on ``tq_skinny_linear_argmax``."""
+        return self.skinny and self.model.skinny_ok(rows) and rows <= ops.SKINNY_LM_HEAD_MAX_ROWS
+
+    def _forward(self, rows: int, ids_only: bool) -> torch.Tensor | None:
         m, s = self.model, self.static
         view = s.view(rows)
         # Embeddings in one launch, source rows resolved on the device.
         x = ops.embed_rows(s.ids[:rows], s.positions[:rows], m.wte.weight, m.wpe.weight, src=s.src[:rows],
                            tokens=s.tokens, error_word=s.error_word)  # fmt: skip
+        if ids_only:
+            # Up to 16 rows, greedy only: the head writes ids, never logits.
+            m.skinny_greedy(x, view, out=s.tokens[:rows])
+            return None
         if self.skinny and m.skinny_ok(rows):
             # Up to 64 rows: five launches per layer, each linear with its LayerNorm / GELU /
             # residual add fused in.
@@ -161,38 +172,41 @@ class DecodeGraphs:
         ops.argmax_rows(logits, out=s.tokens[:rows])
         return logits
 
-    def _capture(self, rows: int) -> None:
+    def _capture(self, rows: int, ids_only: bool) -> None:
         s = self.static
         tokens = s.tokens.clone()  # the warm-up runs overwrite what this step's source rows read
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):  # warm-up launches (same inputs: the K/V writes are idempotent)
             for _ in range(2):
-                self._forward(rows)
+                self._forward(rows, ids_only)
                 s.tokens.copy_(tokens)
         torch.cuda.current_stream().wait_stream(side)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            logits = self._forward(rows)
-        self.graphs[rows] = (graph, logits)
+            logits = self._forward(rows, ids_only)
+        self.graphs[(rows, ids_only)] = (graph, logits)
 
     @torch.no_grad()
-    def launch(self, seqs: list[Sequence], src_rows: list[int] | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    def launch(self, seqs: list[Sequence], src_rows: list[int] | None = None,
+               logits: bool = True) -> tuple[torch.Tensor | None, torch.Tensor]:  # fmt: skip
         """Enqueue one decode step; returns views of its logits ``[n, vocab]`` and greedy ids ``[n]``
         (valid until the next launch) and advances ``num_cached_tokens``. ``src_rows``: see
-        ``StaticDecodeBatch.fill``."""
+        ``StaticDecodeBatch.fill``. ``logits=False``: only the ids are needed; buckets of at most 16
+        rows then run the LM head with the argmax fused in and return None for the logits."""
         rows = bucket_for(len(seqs))
         if rows > self.static.capacity:
             raise ValueError(f"{len(seqs)} sequences exceed the graph capacity {self.static.capacity}")
+        ids_only = not logits and self.fused_greedy(rows)
         self.static.fill(seqs, rows, src_rows)
-        if rows not in self.graphs:
-            self._capture(rows)
-        graph, logits = self.graphs[rows]
+        if (rows, ids_only) not in self.graphs:
+            self._capture(rows, ids_only)
+        graph, out = self.graphs[(rows, ids_only)]
         graph.replay()
         for s in seqs:
             s.num_cached_tokens += 1
         n = len(seqs)
-        return logits[:n], self.static.tokens[:n]
+        return (out[:n] if out is not None else None), self.static.tokens[:n]
 
     def forward(self, seqs: list[Sequence]) -> torch.Tensor:
         """Logits ``[len(seqs), vocab]`` of one decode step; advances ``num_cached_tokens``."""

@@ -113,13 +113,12 @@ class GPT2(nn.Module):
         C = self.cfg.n_embd
         return ops.skinny_supported(rows, C) and ops.skinny_supported(rows, 4 * C)
 
-    def skinny_logits(self, x: torch.Tensor, cache) -> torch.Tensor:
-        """Logits ``[M, vocab]`` of ``M <= ops.SKINNY_MAX_ROWS`` rows from their embeddings ``x``
-        ``[M, C]``, which become the residual stream (updated in place). The reference's loop (tokquay/model.py:172-181) as five
-        launches per block: ``c_attn`` with ``ln_1`` in front, attention, ``c_proj`` adding into x,
-        ``c_fc`` with ``ln_2`` in front and the GELU after, ``mlp.c_proj`` adding into x
-        (``tq_skinny_linear``); then the tied LM head with ``ln_f`` in front, fused up to
-        ``ops.SKINNY_LM_HEAD_MAX_ROWS`` rows, else ``ln_f`` on its own and the head on hipBLASLt."""
+    def skinny_trunk(self, x: torch.Tensor, cache) -> torch.Tensor:
+        """The 12 blocks over ``M <= ops.SKINNY_MAX_ROWS`` rows whose embeddings ``x`` ``[M, C]`` become
+        the residual stream (updated in place and returned). The reference's loop (tokquay/model.py:
+        172-175) as five launches per block: ``c_attn`` with ``ln_1`` in front, attention, ``c_proj``
+        adding into x, ``c_fc`` with ``ln_2`` in front and the GELU after, ``mlp.c_proj`` adding into x
+        (``tq_skinny_linear``)."""
         for i, block in enumerate(self.h):
             at, mlp = block.attn, block.mlp
             qkv = ops.skinny_linear(x, at.c_attn.weight, at.c_attn.bias,
@@ -129,10 +128,26 @@ class GPT2(nn.Module):
             h = ops.skinny_linear(x, mlp.c_fc.weight, mlp.c_fc.bias, ln=(block.ln_2.weight, block.ln_2.bias,
                                                                         block.ln_2.eps), epilogue="gelu")  # fmt: skip
             ops.skinny_linear(h, mlp.c_proj.weight, mlp.c_proj.bias, epilogue="residual", out=x)
+        return x
+
+    def skinny_logits(self, x: torch.Tensor, cache) -> torch.Tensor:
+        """Logits ``[M, vocab]`` of ``M <= ops.SKINNY_MAX_ROWS`` rows from their embeddings ``x``
+        (:meth:`skinny_trunk`), then the tied LM head with ``ln_f`` in front (tokquay/model.py:180-181),
+        fused up to ``ops.SKINNY_LM_HEAD_MAX_ROWS`` rows, else ``ln_f`` on its own and the head on
+        hipBLASLt."""
+        x = self.skinny_trunk(x, cache)
         if x.shape[0] <= ops.SKINNY_LM_HEAD_MAX_ROWS:
             return ops.skinny_linear(x, self.wte.weight, None, ln=(self.ln_f.weight, self.ln_f.bias, self.ln_f.eps))
         _, h = ops.add_layernorm(x, None, self.ln_f.weight, self.ln_f.bias, self.ln_f.eps, x_out=x)
         return h @ self.wte.weight.T
+
+    def skinny_greedy(self, x: torch.Tensor, cache, out: torch.Tensor) -> torch.Tensor:
+        """Greedy ids ``[M]`` of ``M <= ops.SKINNY_LM_HEAD_MAX_ROWS`` rows into ``out`` without logits:
+        :meth:`skinny_trunk`, then ``ln_f``, the tied LM head and the argmax in one launch
+        (``tq_skinny_linear_argmax``; tokquay/model.py:180-181, tokquay/engine.py:190)."""
+        x = self.skinny_trunk(x, cache)
+        return ops.skinny_linear_argmax(x, self.wte.weight, None, ln=(self.ln_f.weight, self.ln_f.bias,
+                                                                      self.ln_f.eps), out=out)  # fmt: skip
 
     def forward(self, input_ids: torch.Tensor, cache: PagedBatch, last_only: bool = False) -> torch.Tensor:
         """input_ids ``[B, T]`` (new tokens, right-padded) -> logits ``[B, T, vocab]``, or ``[B, 1, vocab]``

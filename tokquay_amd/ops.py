@@ -337,6 +337,49 @@ def skinny_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | No
     return out
 
 
+def skinny_linear_argmax(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
+                         ln: tuple[torch.Tensor, torch.Tensor, float] | None = None,
+                         out: torch.Tensor | None = None) -> torch.Tensor:
+    """Greedy ids ``[M]`` (int64) of ``LN(x) @ weight.T + bias`` for at most 16 float32 rows of width
+    768, with no logits written (``tq_skinny_linear_argmax``): the tied LM head with ``ln_f`` in
+    front (tokquay/model.py:180-181) and the batched argmax of Engine._sample (tokquay/engine.py:190)
+    in one launch. Ties keep the lowest column; NaN ranks above every number."""
+    if x.dim() != 2 or x.dtype != torch.float32 or not x.is_cuda or x.stride(1) != 1:
+        raise ValueError("x must be a float32 [rows, K] tensor with contiguous rows on a HIP device")
+    M, K = x.shape
+    if not 0 < M <= SKINNY_LM_HEAD_MAX_ROWS or K != SKINNY_WIDTHS[0]:
+        raise ValueError(f"x must have 1..{SKINNY_LM_HEAD_MAX_ROWS} rows of width {SKINNY_WIDTHS[0]}")
+    if weight.dtype != torch.float32 or weight.device != x.device or weight.dim() != 2 or weight.size(1) != K \
+            or not weight.is_contiguous():
+        raise ValueError(f"weight must be a contiguous float32 [N, {K}] tensor on {x.device}")
+    N = weight.size(0)
+    if bias is not None and (bias.dtype != torch.float32 or bias.device != x.device or bias.shape != (N,)
+                             or not bias.is_contiguous()):
+        raise ValueError(f"bias must be a contiguous float32 [{N}] tensor on {x.device}")
+    gamma = beta = None
+    eps = 0.0
+    if ln is not None:
+        gamma, beta, eps = ln
+        for name, t in (("ln weight", gamma), ("ln bias", beta)):
+            if t.dtype != torch.float32 or t.device != x.device or t.shape != (K,) or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous float32 [{K}] tensor on {x.device}")
+    if out is None:
+        out = torch.empty(M, dtype=torch.int64, device=x.device)
+    elif out.dtype != torch.int64 or out.device != x.device or out.shape != (M,) or (M > 1 and out.stride(0) != 1):
+        raise ValueError(f"out must be an int64 [{M}] tensor on {x.device}")
+    L = _lib.lib()
+    # Slice candidates [M][N / 32] (written before they are read: any contents will do).
+    ws = zeroed_scratch(x.device, "skinny argmax", int(L.tq_skinny_linear_argmax_workspace_size(N)))
+    st = L.tq_skinny_linear_argmax(
+        out.data_ptr(), x.data_ptr(), x.stride(0) if M > 1 else K, M, weight.data_ptr(),
+        bias.data_ptr() if bias is not None else None, N, K,
+        gamma.data_ptr() if gamma is not None else None, beta.data_ptr() if beta is not None else None,
+        float(eps), ws.data_ptr(), ws.numel(), _stream(x.device),
+    )  # fmt: skip
+    _lib.check(st, "tq_skinny_linear_argmax")
+    return out
+
+
 def embed_rows(ids: torch.Tensor, positions: torch.Tensor, wte: torch.Tensor, wpe: torch.Tensor,
                src: torch.Tensor | None = None, tokens: torch.Tensor | None = None,
                error_word: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
