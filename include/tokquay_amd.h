@@ -9,6 +9,8 @@
  *   tq_paged_decode_write  the same, with the new token's cache write folded in
  *                     (tq_paged_decode_write_static: without a workspace argument)
  *   tq_paged_prefill  causal (chunked) prefill attention straight off the pool
+ *   tq_paged_mixed    a step's decode rows (with their cache write) and prefill
+ *                     rows in one launch
  *
  * plus two kernels of the model step around them:
  *
@@ -80,7 +82,8 @@ const char* tq_last_hip_error(void);
 
 /*
  * Arms two hipEvent_t handles (passed as void*; either may be NULL) for the
- * calling thread's next tq_paged_decode, tq_paged_decode_write or tq_paged_prefill call: the start
+ * calling thread's next decode, prefill or mixed attention call (tq_paged_decode,
+ * tq_paged_decode_write, tq_paged_decode_write_static, tq_paged_prefill, tq_paged_mixed): the start
  * event is recorded when that call's first kernel starts and the stop event
  * when its last kernel ends, so hipEventElapsedTime gives the kernels' own
  * duration, without launch gaps. That call disarms them, whatever it returns.
@@ -240,6 +243,52 @@ tq_status tq_paged_prefill(float* out, int64_t out_row_stride,
                            const int32_t* cu_seqlens_q, const int32_t* q_start,
                            int32_t num_seqs, int32_t num_q_rows, int32_t max_query_len,
                            float scale, int32_t* d_error, void* stream);
+
+/*
+ * One step's attention for both kinds of row in one launch: the decode rows as
+ * tq_paged_decode_write computes them (their new K/V written into the pool, then one
+ * query each over its context; the dec_* arguments, context_lens, seq_order, k_new, v_new
+ * and partition_tokens mean what they mean there) and the prefill rows as tq_paged_prefill
+ * computes them (the pre_* arguments, cu_seqlens_q, q_start, num_prefill_seqs, num_q_rows,
+ * max_query_len as there; their K/V must already be in the pool, e.g. by tq_cache_write).
+ * pool, the pool geometry, layer, scale, d_error and stream are shared. The two sets of
+ * sequences must not share a pool slot that the decode rows write.
+ *
+ * The decode rows' waves and the prefill tiles run side by side in one grid, so HBM
+ * streaming and MFMA work overlap and the launch cost is paid once. Every output row is
+ * bit-identical to the corresponding single-kind call's (for the decode rows: the one with
+ * the same partition length; partition_tokens = 0 lets this call choose its own, so compare
+ * with an explicit one). With no prefill rows this is tq_paged_decode_write, with no decode
+ * rows tq_paged_prefill. Needs tq_paged_mixed_workspace_size(...) bytes of workspace
+ * (16-byte aligned; nothing in it needs to start at zero).
+ *
+ * Replaces one Attention.forward call over a batch that holds both decode and prefill rows:
+ * PagedBatch.write + gather + mask + the masked softmax (tokquay/model.py:67-99,
+ * tokquay/kv_cache.py:208-214, :228-242).
+ */
+tq_status tq_paged_mixed(float* dec_out, int64_t dec_out_row_stride,
+                         const float* dec_q, int64_t dec_q_row_stride,
+                         const float* k_new, int64_t k_new_row_stride,
+                         const float* v_new, int64_t v_new_row_stride,
+                         const int32_t* dec_block_tables, int64_t dec_block_table_stride,
+                         int32_t dec_max_blocks_per_seq,
+                         const int32_t* context_lens, const int32_t* seq_order,
+                         int32_t num_decode_seqs, int32_t max_context_len, int32_t partition_tokens,
+                         float* pre_out, int64_t pre_out_row_stride,
+                         const float* pre_q, int64_t pre_q_row_stride,
+                         const int32_t* pre_block_tables, int64_t pre_block_table_stride,
+                         int32_t pre_max_blocks_per_seq,
+                         const int32_t* cu_seqlens_q, const int32_t* q_start,
+                         int32_t num_prefill_seqs, int32_t num_q_rows, int32_t max_query_len,
+                         float* pool, int64_t num_blocks, int32_t num_layers,
+                         int32_t num_heads, int32_t block_size, int32_t head_dim, int32_t layer,
+                         float scale, void* workspace, size_t workspace_bytes,
+                         int32_t* d_error, void* stream);
+
+/* Bytes of workspace tq_paged_mixed needs for these sizes (0 if none). */
+size_t tq_paged_mixed_workspace_size(int32_t num_decode_seqs, int32_t num_heads, int32_t head_dim,
+                                     int32_t max_context_len, int32_t partition_tokens,
+                                     int32_t num_prefill_seqs, int32_t num_q_rows, int32_t max_query_len);
 
 /*
  * Greedy sampling over a batch of logit rows:

@@ -214,6 +214,139 @@ def test_mixed_chunked_prefill_and_decode(chunk):
     check(sc, brute=False)
 
 
+# ------------------------------------------------------------------------------ one launch for mixed steps
+def mixed_case(name: str):
+    """(starts, new_lens) of a step with prefill rows first, then decode rows."""
+    rng = random.Random(hash(name) % 1000)
+    if name == "config5-chunk1":  # 768 prefill tiles: 4 waves per tile
+        pre = [(256, 256)] * 4
+        dec = [rng.randint(64, 768) for _ in range(128)]
+    elif name == "tail-chunk":  # 3 short tails at 768: 8 waves per tile
+        pre = [(768, 5), (768, 102), (768, 9)]
+        dec = [rng.randint(64, 768) for _ in range(128)]
+    elif name == "wide-prefill":  # 8 x 600-row prompts: 3,648 tiles, 1 wave per tile
+        pre = [(0, 600)] * 8
+        dec = [rng.randint(16, 300) for _ in range(16)]
+    elif name == "long-decoders":  # contexts past 1024 positions: several partitions and a merge
+        pre = [(40, 37), (0, 3)]
+        dec = [1500, 2100, 17, 1025, 1, 64]
+    else:  # "tiny"
+        pre = [(0, 3)]
+        dec = [5]
+    starts = [s for s, _ in pre] + [c - 1 for c in dec]
+    lens = [n for _, n in pre] + [1] * len(dec)
+    return starts, lens
+
+
+def run_mixed_modes(sc: Scenario, partition_tokens: int, hook: bool = False):
+    """run_product with the one-launch mixed path off, then on (optionally through the per-kernel
+    ctypes path, which a launch hook selects)."""
+    from tokquay_amd.kv_cache import PagedBatch
+
+    kinds = []
+    res = []
+    try:
+        for one in (False, True):
+            PagedBatch.one_launch_mixed = one
+            PagedBatch.launch_hook = (lambda batch, kind: kinds.append(kind)) if hook else None
+            res.append(sc.run_product(partition_tokens))
+    finally:
+        PagedBatch.one_launch_mixed = True
+        PagedBatch.launch_hook = None
+    return res, kinds
+
+
+@pytest.mark.parametrize("name", ["config5-chunk1", "tail-chunk", "wide-prefill", "long-decoders", "tiny"])
+@pytest.mark.parametrize("block_size", [8, 16, 32])
+@pytest.mark.parametrize("partition_tokens", [64, 1024])
+def test_one_launch_mixed_equals_two_launches(name, block_size, partition_tokens):
+    """tq_paged_mixed == tq_paged_decode_write + tq_paged_prefill, bit for bit (outputs and pool), at an
+    explicit partition length (the decode rows' rounding depends on it)."""
+    starts, lens = mixed_case(name)
+    sc = Scenario(starts, lens, block_size=block_size, n_layer=2, layer=1, seed=block_size + len(starts))
+    (pool_a, out_a, batch), (pool_b, out_b, _) = run_mixed_modes(sc, partition_tokens)[0]
+    assert batch.num_decode > 0 and batch.num_prefill > 0
+    assert torch.equal(out_a, out_b)
+    assert torch.equal(pool_a, pool_b)
+
+
+@pytest.mark.parametrize("name", ["config5-chunk1", "tail-chunk", "long-decoders", "tiny"])
+@pytest.mark.parametrize("block_size", [16, 32])
+def test_one_launch_mixed_matches_the_reference(name, block_size):
+    """The default path (one launch, partitions chosen for the mixed grid) against the reference's
+    gather path and float64 brute force."""
+    starts, lens = mixed_case(name)
+    sc = Scenario(starts, lens, block_size=block_size, seed=3 + block_size)
+    check(sc, brute=name != "config5-chunk1")
+
+
+def test_one_launch_mixed_through_the_per_kernel_path():
+    """The ctypes per-kernel path (taken when a launch hook is set) makes the same single launch."""
+    starts, lens = mixed_case("tail-chunk")
+    sc = Scenario(starts, lens, block_size=16, seed=9)
+    res, kinds = run_mixed_modes(sc, 0, hook=True)
+    assert kinds == ["decode", "prefill", "mixed"]
+    ref_pool, ref_out, _ = sc.run_product(0)  # the native path, one launch
+    assert torch.equal(res[1][1], ref_out) and torch.equal(res[1][0], ref_pool)
+
+
+def test_mixed_entry_point_with_one_side_empty_and_bad_arguments():
+    """No prefill rows: tq_paged_decode_write's launch; no decode rows: tq_paged_prefill's; negative sizes
+    and a missing k_new are refused before anything is launched."""
+    from tokquay_amd import _lib, ops
+
+    starts, lens = mixed_case("long-decoders")
+    sc = Scenario(starts, lens, block_size=16, seed=4)
+    pool, out_ref, batch = sc.run_product(0)
+    Bp = batch.num_prefill
+    qkv = sc.packed_qkv(batch.token_index).cuda()
+    C = 768
+    Nd = batch.num_decode
+    N = batch.num_tokens
+    # Packed rows: decode rows first, then the prefill rows.
+    dq, dk, dv = qkv[:Nd, :C], qkv[:Nd, C : 2 * C], qkv[:Nd, 2 * C :]
+    pq = qkv[Nd:, :C]
+    dtab = torch.tensor([sc.tables[b] + [0] * (200 - len(sc.tables[b])) for b in range(Bp, Bp + Nd)], dtype=torch.int32).cuda()
+    ptab = torch.tensor([sc.tables[b] + [0] * (200 - len(sc.tables[b])) for b in range(Bp)], dtype=torch.int32).cuda()
+    dctx = torch.tensor([sc.ctxs[b] for b in range(Bp, Bp + Nd)], dtype=torch.int32, device="cuda")
+    cu = torch.tensor([0] + list(np.cumsum(sc.new_lens[:Bp])), dtype=torch.int32, device="cuda")
+    qst = torch.tensor(sc.starts[:Bp], dtype=torch.int32, device="cuda")
+    maxc, maxq = int(dctx.max()), max(sc.new_lens[:Bp])
+
+    # Decode rows only (no prefill rows): the same bits as paged_decode with k_new / v_new.
+    p1, p2 = sc.pool.cuda(), sc.pool.cuda()
+    o1, o2 = torch.empty(Nd, C, device="cuda"), torch.empty(Nd, C, device="cuda")
+    ops.paged_decode(o1, dq, p1, sc.layer, dtab, dctx, maxc, k_new=dk, v_new=dv)
+    empty_cu = torch.zeros(1, dtype=torch.int32, device="cuda")
+    empty_st = torch.zeros(0, dtype=torch.int32, device="cuda")
+    ops.paged_mixed(o2, dq, dk, dv, dtab, dctx, maxc, torch.empty(0, C, device="cuda"), torch.empty(0, C, device="cuda"),
+                    torch.zeros(0, 200, dtype=torch.int32, device="cuda"), empty_cu, empty_st, 0, p2, sc.layer)  # fmt: skip
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(p1, p2)
+
+    # Both sides through ops.paged_mixed: the same bits as PagedBatch.attend's one launch.
+    p3 = sc.pool.cuda()
+    slots = []
+    for b in range(Bp):
+        for t in range(sc.new_lens[b]):
+            pos = sc.starts[b] + t
+            slots.append(sc.tables[b][pos // 16] * 16 + pos % 16)
+    ops.cache_write(p3, sc.layer, qkv[Nd:, C : 2 * C], qkv[Nd:, 2 * C :], torch.tensor(slots, device="cuda"))
+    o3d, o3p = torch.empty(Nd, C, device="cuda"), torch.empty(N - Nd, C, device="cuda")
+    ops.paged_mixed(o3d, dq, dk, dv, dtab, dctx, maxc, o3p, pq, ptab, cu, qst, maxq, p3, sc.layer)
+    torch.cuda.synchronize()
+    assert torch.equal(torch.cat([o3d, o3p]).cpu(), out_ref) and torch.equal(p3.cpu(), pool)
+
+    # Argument errors come back as status codes and launch nothing.
+    L = _lib.lib()
+    bad = [0] * 40
+    bad[13] = -1  # num_decode_seqs
+    assert L.tq_paged_mixed(*bad) == 1
+    assert L.tq_paged_mixed_workspace_size(4, 12, 64, 3000, 0, 0, 0, 0) == L.tq_paged_decode_workspace_size(4, 12, 64, 3000, 0)
+    with pytest.raises(ValueError):
+        ops.paged_mixed(o3d, dq, dk, dv, dtab, dctx, maxc, o3p, pq, ptab, cu[:-1], qst, maxq, p3, sc.layer)
+
+
 # ------------------------------------------------------------------------------ contract edges
 def test_write_contract_padded_layout_is_bit_exact_and_padding_never_writes():
     """BatchedKV.write with the reference's [B, H, T, d] layout: padded positions write nothing and

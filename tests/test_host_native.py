@@ -136,7 +136,7 @@ def test_validation_order_and_messages(nat):
 
 
 def test_attend_entry_rejects_bad_sizes_without_launching(nat):
-    args = [0] * 29
+    args = [0] * 30
     args[9] = 0.125
     args[12] = 0  # N = 0
     with pytest.raises(ValueError):

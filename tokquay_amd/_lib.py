@@ -103,6 +103,25 @@ SIGNATURES: dict[str, tuple] = {
             ctypes.c_float, c_i32p, ctypes.c_void_p,  # scale, d_error, stream
         ],
     ),
+    "tq_paged_mixed": (
+        ctypes.c_int,
+        [
+            c_f32p, ctypes.c_int64, c_f32p, ctypes.c_int64,  # dec_out, dec_out_row_stride, dec_q, dec_q_row_stride
+            c_f32p, ctypes.c_int64, c_f32p, ctypes.c_int64,  # k_new, k_new_row_stride, v_new, v_new_row_stride
+            c_i32p, ctypes.c_int64, ctypes.c_int32,  # dec_block_tables, dec_block_table_stride, dec_max_blocks_per_seq
+            c_i32p, c_i32p,  # context_lens, seq_order
+            ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,  # num_decode_seqs, max_context_len, partition_tokens
+            c_f32p, ctypes.c_int64, c_f32p, ctypes.c_int64,  # pre_out, pre_out_row_stride, pre_q, pre_q_row_stride
+            c_i32p, ctypes.c_int64, ctypes.c_int32,  # pre_block_tables, pre_block_table_stride, pre_max_blocks_per_seq
+            c_i32p, c_i32p,  # cu_seqlens_q, q_start
+            ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,  # num_prefill_seqs, num_q_rows, max_query_len
+            c_f32p, ctypes.c_int64, ctypes.c_int32,  # pool, num_blocks, num_layers
+            ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,  # num_heads, block_size, head_dim, layer
+            ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t,  # scale, workspace, workspace_bytes
+            c_i32p, ctypes.c_void_p,  # d_error, stream
+        ],
+    ),
+    "tq_paged_mixed_workspace_size": (ctypes.c_size_t, [ctypes.c_int32] * 8),
     "tq_add_layernorm": (
         ctypes.c_int,
         [

@@ -7,7 +7,8 @@
 //   view's constructor, tokquay/kv_cache.py:174-226 (validation :182-191, padded
 //   tables :195-200, slots :216-226), restated for packed rows.
 // * attend(): one layer's attention launches in one call - decode rows through
-//   tq_paged_decode_write, then the multi-token rows' cache write and prefill.
+//   tq_paged_decode_write, then the multi-token rows' cache write and prefill; with both
+//   kinds of row, the cache write and one tq_paged_mixed launch for both.
 // * fill_decode(): the captured decode step's fixed-address metadata, straight from
 //   the Sequence objects (token ids, positions, source rows, block tables, context
 //   lengths, dispatch order), padded to the graph's bucket.
@@ -221,19 +222,21 @@ PyObject* py_fill(PyObject*, PyObject* args) {
 
 // attend(out, qkv, pool, num_blocks, num_layers, num_heads, block_size, head_dim, layer, scale, stream,
 //        error_word, N, Bd, dec_tables, nbd, dec_ctx, dec_order, decode_max_ctx, partition_tokens,
-//        workspace, workspace_bytes, Bp, slot_mapping, pre_tables, nbp, pre_cu, pre_start, prefill_max_q)
+//        workspace, workspace_bytes, Bp, slot_mapping, pre_tables, nbp, pre_cu, pre_start, prefill_max_q,
+//        mixed)
 // launches one layer's kernels for a packed batch (device pointers and the stream as Python ints).
 // Returns None, or (status, entry point name) for the first launch that failed.
 PyObject* py_attend(PyObject*, PyObject* args) {
   unsigned long long out, qkv, pool, stream, d_error, dec_tables, dec_ctx, dec_order, workspace, slot_mapping,
       pre_tables, pre_cu, pre_start;
   long long num_blocks, N, Bd, nbd, decode_max_ctx, ws_bytes, Bp, nbp, prefill_max_q;
-  int num_layers, num_heads, block_size, head_dim, layer, partition_tokens;
+  int num_layers, num_heads, block_size, head_dim, layer, partition_tokens, mixed;
   float scale;
-  if (!PyArg_ParseTuple(args, "KKKLiiiiifKKLLKLKKLiKLLKKLKKL", &out, &qkv, &pool, &num_blocks, &num_layers,
+  if (!PyArg_ParseTuple(args, "KKKLiiiiifKKLLKLKKLiKLLKKLKKLp", &out, &qkv, &pool, &num_blocks, &num_layers,
                         &num_heads, &block_size, &head_dim, &layer, &scale, &stream, &d_error, &N, &Bd,
                         &dec_tables, &nbd, &dec_ctx, &dec_order, &decode_max_ctx, &partition_tokens, &workspace,
-                        &ws_bytes, &Bp, &slot_mapping, &pre_tables, &nbp, &pre_cu, &pre_start, &prefill_max_q))
+                        &ws_bytes, &Bp, &slot_mapping, &pre_tables, &nbp, &pre_cu, &pre_start, &prefill_max_q,
+                        &mixed))
     return nullptr;
   if (N < 1 || Bd < 0 || Bp < 0 || nbd < 0 || nbp < 0 || ws_bytes < 0) {
     PyErr_SetString(PyExc_ValueError, "attend: negative sizes");
@@ -249,25 +252,44 @@ PyObject* py_attend(PyObject*, PyObject* args) {
   tq_status s = TQ_OK;
   const char* what = nullptr;
   Py_BEGIN_ALLOW_THREADS
-  if (Bd > 0) {
-    s = tq_paged_decode_write(o, C, q, row3, q + C, row3, q + 2 * C, row3, pl, num_blocks, num_layers, num_heads,
-                              block_size, head_dim, layer, reinterpret_cast<const int32_t*>(dec_tables), nbd,
-                              (int32_t)nbd, reinterpret_cast<const int32_t*>(dec_ctx),
-                              reinterpret_cast<const int32_t*>(dec_order), (int32_t)Bd, (int32_t)decode_max_ctx,
-                              scale, partition_tokens, reinterpret_cast<void*>(workspace), (size_t)ws_bytes, err, st);
-    if (s != TQ_OK) what = "tq_paged_decode_write";
-  }
-  if (s == TQ_OK && Bp > 0) {
-    const float* qp = q + Bd * row3;
+  const float* qp = q + Bd * row3;  // the first prefill row
+  const int64_t* pre_slots = reinterpret_cast<const int64_t*>(slot_mapping) + Bd;
+  if (mixed && Bd > 0 && Bp > 0) {
     s = tq_cache_write(pl, num_blocks, num_layers, num_heads, block_size, head_dim, layer, qp + C, row3, qp + 2 * C,
-                       row3, reinterpret_cast<const int64_t*>(slot_mapping) + Bd, N - Bd, err, st);
+                       row3, pre_slots, N - Bd, err, st);
     if (s != TQ_OK) what = "tq_cache_write";
     if (s == TQ_OK) {
-      s = tq_paged_prefill(o + Bd * C, C, qp, row3, pl, num_blocks, num_layers, num_heads, block_size, head_dim,
-                           layer, reinterpret_cast<const int32_t*>(pre_tables), nbp, (int32_t)nbp,
-                           reinterpret_cast<const int32_t*>(pre_cu), reinterpret_cast<const int32_t*>(pre_start),
-                           (int32_t)Bp, (int32_t)(N - Bd), (int32_t)prefill_max_q, scale, err, st);
-      if (s != TQ_OK) what = "tq_paged_prefill";
+      s = tq_paged_mixed(o, C, q, row3, q + C, row3, q + 2 * C, row3, reinterpret_cast<const int32_t*>(dec_tables),
+                         nbd, (int32_t)nbd, reinterpret_cast<const int32_t*>(dec_ctx),
+                         reinterpret_cast<const int32_t*>(dec_order), (int32_t)Bd, (int32_t)decode_max_ctx,
+                         partition_tokens, o + Bd * C, C, qp, row3, reinterpret_cast<const int32_t*>(pre_tables), nbp,
+                         (int32_t)nbp, reinterpret_cast<const int32_t*>(pre_cu),
+                         reinterpret_cast<const int32_t*>(pre_start), (int32_t)Bp, (int32_t)(N - Bd),
+                         (int32_t)prefill_max_q, pl, num_blocks, num_layers, num_heads, block_size, head_dim, layer,
+                         scale, reinterpret_cast<void*>(workspace), (size_t)ws_bytes, err, st);
+      if (s != TQ_OK) what = "tq_paged_mixed";
+    }
+  } else {
+    if (Bd > 0) {
+      s = tq_paged_decode_write(o, C, q, row3, q + C, row3, q + 2 * C, row3, pl, num_blocks, num_layers, num_heads,
+                                block_size, head_dim, layer, reinterpret_cast<const int32_t*>(dec_tables), nbd,
+                                (int32_t)nbd, reinterpret_cast<const int32_t*>(dec_ctx),
+                                reinterpret_cast<const int32_t*>(dec_order), (int32_t)Bd, (int32_t)decode_max_ctx,
+                                scale, partition_tokens, reinterpret_cast<void*>(workspace), (size_t)ws_bytes, err,
+                                st);
+      if (s != TQ_OK) what = "tq_paged_decode_write";
+    }
+    if (s == TQ_OK && Bp > 0) {
+      s = tq_cache_write(pl, num_blocks, num_layers, num_heads, block_size, head_dim, layer, qp + C, row3,
+                         qp + 2 * C, row3, pre_slots, N - Bd, err, st);
+      if (s != TQ_OK) what = "tq_cache_write";
+      if (s == TQ_OK) {
+        s = tq_paged_prefill(o + Bd * C, C, qp, row3, pl, num_blocks, num_layers, num_heads, block_size, head_dim,
+                             layer, reinterpret_cast<const int32_t*>(pre_tables), nbp, (int32_t)nbp,
+                             reinterpret_cast<const int32_t*>(pre_cu), reinterpret_cast<const int32_t*>(pre_start),
+                             (int32_t)Bp, (int32_t)(N - Bd), (int32_t)prefill_max_q, scale, err, st);
+        if (s != TQ_OK) what = "tq_paged_prefill";
+      }
     }
   }
   Py_END_ALLOW_THREADS

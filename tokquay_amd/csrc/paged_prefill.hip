@@ -37,6 +37,9 @@
 #include <hip/hip_ext.h>
 #include <math.h>
 
+#include <algorithm>
+
+#include "decode_wave.h"
 #include "tq_internal.h"
 
 namespace tq {
@@ -91,9 +94,9 @@ constexpr int kRound = 64;    // dispatches per XCD taken as one round (two per 
 // against contiguous runs with the last query tiles first; rounds of 32 or 128 do
 // about as well, 16 worse; dealing contiguous runs of groups instead of every
 // eighth group left a 3-prompt chunk with one long prompt 45 % slower). Returns
-// false for a padding workgroup.
-__device__ __forceinline__ bool tile_of(const PrefillArgs& a, int& qt, int& h, int& b) {
-  const int p = blockIdx.x;
+// false for a padding workgroup. `p` is the workgroup's index among the launch's prefill
+// workgroups, a multiple of 8 dispatches after the first (so p % 8 is still its XCD).
+__device__ __forceinline__ bool tile_of(const PrefillArgs& a, int p, int& qt, int& h, int& b) {
   const int xcd = p % kXcds, local = p / kXcds;
   const int G = (a.groups - xcd + kXcds - 1) / kXcds;  // groups xcd, xcd + 8, ... on this XCD
   const int n = G * a.qtiles;
@@ -201,14 +204,16 @@ __device__ __forceinline__ void load_kv_block_tile(const PrefillArgs& a, const f
   }
 }
 
+// The work of prefill workgroup `dispatch` (its KS waves): one query tile of one head of one
+// sequence, or nothing for a padding workgroup.
 template <int BS_CT, int KS>
-__global__ __launch_bounds__(kWave* KS) void prefill_kernel(const PrefillArgs a) {
+__device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int dispatch) {
   const int lane = threadIdx.x & (kWave - 1);
   // Wave-uniform by construction; readfirstlane lets the compiler keep the key-tile loop
   // (counter, bounds, branches) in scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   int qt, h, b;
-  if (!tile_of(a, qt, h, b)) return;  // padding workgroup (uniform)
+  if (!tile_of(a, dispatch, qt, h, b)) return;  // padding workgroup (uniform)
   const int bs = BS_CT > 0 ? BS_CT : a.block_size;
 
   const int row0 = a.cu_q[b];
@@ -467,6 +472,11 @@ __global__ __launch_bounds__(kWave* KS) void prefill_kernel(const PrefillArgs a)
   }
 }
 
+template <int BS_CT, int KS>
+__global__ __launch_bounds__(kWave* KS) void prefill_kernel(const PrefillArgs a) {
+  prefill_workgroup<BS_CT, KS>(a, blockIdx.x);
+}
+
 // The 8-wave instance reserves this much extra (unused) LDS per workgroup so that a
 // CU holds only one of them: the round-robin dispatcher otherwise put a second busy
 // workgroup on a CU whose first one was still running while other CUs sat idle
@@ -510,6 +520,155 @@ void launch_prefill(const PrefillArgs& a, hipStream_t stream, hipEvent_t start, 
   }
 }
 
+// A prefill call's arguments as the C ABI passes them.
+struct PrefillCall {
+  float* out;
+  int64_t out_row_stride;
+  const float* q;
+  int64_t q_row_stride;
+  const float* pool;
+  int64_t num_blocks;
+  int32_t num_layers, num_heads, block_size, head_dim, layer;
+  const int32_t* block_tables;
+  int64_t block_table_stride;
+  int32_t max_blocks_per_seq;
+  const int32_t* cu_seqlens_q;
+  const int32_t* q_start;
+  int32_t num_seqs, num_q_rows, max_query_len;
+  float scale;
+  int32_t* d_error;
+};
+
+// Validates a prefill call and fills `a`. TQ_OK with `empty` set: nothing to launch.
+tq_status make_prefill_args(const PrefillCall& c, PrefillArgs& a, bool& empty) {
+  empty = true;
+  if (c.num_seqs < 0 || c.num_blocks < 1 || c.num_layers < 1 || c.num_heads < 1 || c.block_size < 1 ||
+      c.head_dim < 1 || c.layer < 0 || c.layer >= c.num_layers || c.max_blocks_per_seq < 0 ||
+      c.num_q_rows < 0 || c.max_query_len < 0 || c.num_blocks > 0x7fffffffLL)
+    return TQ_ERR_INVALID_ARGUMENT;
+  if (c.head_dim != kHeadDim || c.block_size > kMaxBlockSize) return TQ_ERR_UNSUPPORTED;
+  if (c.num_seqs == 0 || c.num_q_rows == 0 || c.max_query_len == 0) return TQ_OK;
+  if (c.out == nullptr || c.q == nullptr || c.pool == nullptr || c.block_tables == nullptr ||
+      c.cu_seqlens_q == nullptr || c.q_start == nullptr)
+    return TQ_ERR_INVALID_ARGUMENT;
+  const int64_t row = (int64_t)c.num_heads * c.head_dim;
+  if (c.out_row_stride < row || c.q_row_stride < row || c.block_table_stride < c.max_blocks_per_seq)
+    return TQ_ERR_INVALID_ARGUMENT;
+  if (((uintptr_t)c.out | (uintptr_t)c.q | (uintptr_t)c.pool) % 16 != 0 || c.out_row_stride % 4 != 0 ||
+      c.q_row_stride % 4 != 0)
+    return TQ_ERR_INVALID_ARGUMENT;
+  const int64_t qtiles = ((int64_t)c.max_query_len + kTile - 1) / kTile;
+  if ((qtiles * c.num_heads * c.num_seqs + kXcds * qtiles) > 0x7fffffffLL) return TQ_ERR_UNSUPPORTED;
+  if ((int64_t)c.max_blocks_per_seq * c.block_size > 0x7fffffffLL) return TQ_ERR_UNSUPPORTED;
+
+  const PoolGeom g = pool_geom(c.num_layers, c.num_heads, c.block_size, c.head_dim, c.layer);
+  a = PrefillArgs{};
+  a.out = c.out;
+  a.out_stride = c.out_row_stride;
+  a.q = c.q;
+  a.q_stride = c.q_row_stride;
+  a.pool_layer = c.pool + g.layer_offset;
+  a.block_stride = g.block_stride;
+  a.kv_stride = g.kv_stride;
+  a.head_stride = g.head_stride;
+  a.block_tables = c.block_tables;
+  a.bt_stride = c.block_table_stride;
+  a.cu_q = c.cu_seqlens_q;
+  a.q_start = c.q_start;
+  a.d_error = c.d_error;
+  a.scale = c.scale;
+  a.num_blocks = (int32_t)c.num_blocks;
+  a.num_heads = c.num_heads;
+  a.block_size = c.block_size;
+  a.max_blocks = c.max_blocks_per_seq;
+  a.num_q_rows = c.num_q_rows;
+  a.qtiles = (int32_t)qtiles;
+  a.num_seqs = c.num_seqs;
+  const int64_t groups = (int64_t)c.num_heads * c.num_seqs;
+  a.groups = (int32_t)groups;
+  a.total = (int32_t)(kXcds * ((groups + kXcds - 1) / kXcds) * qtiles);
+  empty = false;
+  return TQ_OK;
+}
+
+// ---------------------------------------------------------------------------- mixed launch
+
+// Waves per workgroup of a prefill launch of these sizes.
+int prefill_key_split(int32_t num_seqs, int32_t num_heads, int32_t max_query_len) {
+  return choose_key_split((int64_t)num_heads * num_seqs * (((int64_t)max_query_len + kTile - 1) / kTile));
+}
+
+// Dispatch order of a mixed launch: blocks of 8 workgroups (one per XCD) alternate between
+// decode and prefill work while both kinds last, then the longer kind's remaining blocks
+// follow, so HBM-bound decode waves and MFMA-bound prefill waves share the CUs from the
+// start instead of one kind filling the GPU first. Returns true for a decode workgroup; idx
+// is the workgroup's index among its own kind, with idx % 8 == bx % 8 (its XCD).
+__device__ __forceinline__ bool mixed_slot(int bx, int decode_groups, int prefill_groups, int& idx) {
+  const int blk = bx / kXcds, x = bx - blk * kXcds;
+  const int pairs = min(decode_groups, prefill_groups) / kXcds;  // both are multiples of 8
+  if (blk < 2 * pairs) {
+    idx = (blk >> 1) * kXcds + x;
+    return (blk & 1) == 0;
+  }
+  idx = (blk - pairs) * kXcds + x;
+  return decode_groups > prefill_groups;
+}
+
+// One launch for a step's decode rows and its prefill tiles (the reference runs both kinds of
+// row through one attention call, tokquay/model.py:67-99). Decode streams K/V from HBM and
+// barely touches the matrix cores; prefill is MFMA work on L2-resident tiles: CUs that hold
+// waves of both kinds run them side by side, and the launch's start-up and drain are paid
+// once instead of twice. Decode workgroup i takes, with d.split_waves == KS, the i-th
+// (sequence in seq_order, head) pair with its KS waves splitting the context (as the decode
+// launch's small-batch kernel does); otherwise its waves take one unit each, unit u being head
+// u % H of partition (u / H) % parts of the sequence listed (u / H) / parts-th (as the decode
+// partition kernel). Prefill workgroups are the prefill launch's own. Per unit and per tile
+// the code is the decode and prefill kernels', so each output row is bit-identical to the
+// corresponding single-kind launch's.
+template <int DEC_BS, int PRE_BS, int KS>
+__global__ __launch_bounds__(kWave* KS) void mixed_kernel(const PrefillArgs p, const DecodeArgs d,
+                                                          int32_t decode_groups, int32_t decode_units) {
+  int idx;
+  if (mixed_slot((int)blockIdx.x, decode_groups, p.total, idx)) {  // uniform across the workgroup
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    if (d.split_waves > 0) {
+      if (idx >= decode_units) return;  // uniform: a padding workgroup
+      const int seq = idx / d.num_heads;
+      decode_group<DEC_BS, true, KS>(d, seq, idx - seq * d.num_heads, wave, lane);
+      return;
+    }
+    const int u = idx * KS + wave;
+    if (u >= decode_units) return;  // whole wave; partition units meet no barrier
+    const int rest = u / d.num_heads;
+    decode_unit<DEC_BS, true>(d, rest / d.max_parts, u - rest * d.num_heads, rest % d.max_parts, lane);
+    return;
+  }
+  prefill_workgroup<PRE_BS, KS>(p, idx);
+}
+
+template <int DEC_BS, int PRE_BS, int KS>
+void launch_mixed_ks(const PrefillArgs& p, const DecodeArgs& d, int32_t groups, int32_t units, hipStream_t stream,
+                     hipEvent_t start, hipEvent_t stop) {
+  const dim3 grid((unsigned)(groups + p.total)), block(kWave * KS);
+  if (start == nullptr && stop == nullptr)
+    hipLaunchKernelGGL((mixed_kernel<DEC_BS, PRE_BS, KS>), grid, block, 0, stream, p, d, groups, units);
+  else
+    hipExtLaunchKernelGGL((mixed_kernel<DEC_BS, PRE_BS, KS>), grid, block, 0, stream, start, stop, 0, p, d, groups,
+                          units);
+}
+
+template <int DEC_BS, int PRE_BS>
+void launch_mixed(const PrefillArgs& p, const DecodeArgs& d, int ks, int32_t groups, int32_t units,
+                  hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+  switch (ks) {
+    case 1: launch_mixed_ks<DEC_BS, PRE_BS, 1>(p, d, groups, units, stream, start, stop); break;
+    case 2: launch_mixed_ks<DEC_BS, PRE_BS, 2>(p, d, groups, units, stream, start, stop); break;
+    case 4: launch_mixed_ks<DEC_BS, PRE_BS, 4>(p, d, groups, units, stream, start, stop); break;
+    default: launch_mixed_ks<DEC_BS, PRE_BS, 8>(p, d, groups, units, stream, start, stop); break;
+  }
+}
+
 }  // namespace
 }  // namespace tq
 
@@ -523,56 +682,101 @@ extern "C" tq_status tq_paged_prefill(float* out, int64_t out_row_stride, const 
                                       float scale, int32_t* d_error, void* stream) {
   using namespace tq;
   const TimingEvents timing = take_timing_events();  // for this call only, whatever it returns
-  if (num_seqs < 0 || num_blocks < 1 || num_layers < 1 || num_heads < 1 || block_size < 1 ||
-      head_dim < 1 || layer < 0 || layer >= num_layers || max_blocks_per_seq < 0 ||
-      num_q_rows < 0 || max_query_len < 0 || num_blocks > 0x7fffffffLL)
-    return TQ_ERR_INVALID_ARGUMENT;
-  if (head_dim != kHeadDim || block_size > kMaxBlockSize) return TQ_ERR_UNSUPPORTED;
-  if (num_seqs == 0 || num_q_rows == 0 || max_query_len == 0) return TQ_OK;
-  if (out == nullptr || q == nullptr || pool == nullptr || block_tables == nullptr ||
-      cu_seqlens_q == nullptr || q_start == nullptr)
-    return TQ_ERR_INVALID_ARGUMENT;
-  const int64_t row = (int64_t)num_heads * head_dim;
-  if (out_row_stride < row || q_row_stride < row || block_table_stride < max_blocks_per_seq)
-    return TQ_ERR_INVALID_ARGUMENT;
-  if (((uintptr_t)out | (uintptr_t)q | (uintptr_t)pool) % 16 != 0 || out_row_stride % 4 != 0 ||
-      q_row_stride % 4 != 0)
-    return TQ_ERR_INVALID_ARGUMENT;
-  const int64_t qtiles = ((int64_t)max_query_len + kTile - 1) / kTile;
-  if ((qtiles * num_heads * num_seqs + kXcds * qtiles) > 0x7fffffffLL) return TQ_ERR_UNSUPPORTED;
-  if ((int64_t)max_blocks_per_seq * block_size > 0x7fffffffLL) return TQ_ERR_UNSUPPORTED;
-
-  const PoolGeom g = pool_geom(num_layers, num_heads, block_size, head_dim, layer);
   PrefillArgs a;
-  a.out = out;
-  a.out_stride = out_row_stride;
-  a.q = q;
-  a.q_stride = q_row_stride;
-  a.pool_layer = pool + g.layer_offset;
-  a.block_stride = g.block_stride;
-  a.kv_stride = g.kv_stride;
-  a.head_stride = g.head_stride;
-  a.block_tables = block_tables;
-  a.bt_stride = block_table_stride;
-  a.cu_q = cu_seqlens_q;
-  a.q_start = q_start;
-  a.d_error = d_error;
-  a.scale = scale;
-  a.num_blocks = (int32_t)num_blocks;
-  a.num_heads = num_heads;
-  a.block_size = block_size;
-  a.max_blocks = max_blocks_per_seq;
-  a.num_q_rows = num_q_rows;
-  a.qtiles = (int32_t)qtiles;
-  a.num_seqs = num_seqs;
-  const int64_t groups = (int64_t)num_heads * num_seqs;
-  a.groups = (int32_t)groups;
-  a.total = (int32_t)(kXcds * ((groups + kXcds - 1) / kXcds) * qtiles);
-
+  bool empty;
+  const tq_status st = make_prefill_args({out, out_row_stride, q, q_row_stride, pool, num_blocks, num_layers,
+                                          num_heads, block_size, head_dim, layer, block_tables, block_table_stride,
+                                          max_blocks_per_seq, cu_seqlens_q, q_start, num_seqs, num_q_rows,
+                                          max_query_len, scale, d_error},
+                                         a, empty);
+  if (st != TQ_OK || empty) return st;
   hipStream_t s = (hipStream_t)stream;
   switch (block_size) {
     case 16: launch_prefill<16>(a, s, timing.start, timing.stop); break;
     default: launch_prefill<0>(a, s, timing.start, timing.stop); break;
   }
+  return check_launch();
+}
+
+extern "C" size_t tq_paged_mixed_workspace_size(int32_t num_decode_seqs, int32_t num_heads, int32_t head_dim,
+                                                int32_t max_context_len, int32_t partition_tokens,
+                                                int32_t num_prefill_seqs, int32_t num_q_rows, int32_t max_query_len) {
+  using namespace tq;
+  if (num_prefill_seqs <= 0 || num_q_rows <= 0 || max_query_len <= 0)
+    return tq_paged_decode_workspace_size(num_decode_seqs, num_heads, head_dim, max_context_len, partition_tokens);
+  if (num_decode_seqs <= 0 || num_heads <= 0 || head_dim != kHeadDim || max_context_len <= 0) return 0;
+  if (partition_tokens < 0 || partition_tokens % kChunk != 0 || partition_tokens > kMaxPartition) return 0;
+  const int ks = prefill_key_split(num_prefill_seqs, num_heads, max_query_len);
+  return decode_workspace_bytes(num_decode_seqs, num_heads,
+                                decode_grid(num_decode_seqs, num_heads, max_context_len, partition_tokens, ks));
+}
+
+extern "C" tq_status tq_paged_mixed(float* dec_out, int64_t dec_out_row_stride, const float* dec_q,
+                                    int64_t dec_q_row_stride, const float* k_new, int64_t k_new_row_stride,
+                                    const float* v_new, int64_t v_new_row_stride, const int32_t* dec_block_tables,
+                                    int64_t dec_block_table_stride, int32_t dec_max_blocks_per_seq,
+                                    const int32_t* context_lens, const int32_t* seq_order, int32_t num_decode_seqs,
+                                    int32_t max_context_len, int32_t partition_tokens, float* pre_out,
+                                    int64_t pre_out_row_stride, const float* pre_q, int64_t pre_q_row_stride,
+                                    const int32_t* pre_block_tables, int64_t pre_block_table_stride,
+                                    int32_t pre_max_blocks_per_seq, const int32_t* cu_seqlens_q,
+                                    const int32_t* q_start, int32_t num_prefill_seqs, int32_t num_q_rows,
+                                    int32_t max_query_len, float* pool, int64_t num_blocks, int32_t num_layers,
+                                    int32_t num_heads, int32_t block_size, int32_t head_dim, int32_t layer,
+                                    float scale, void* workspace, size_t workspace_bytes, int32_t* d_error,
+                                    void* stream) {
+  using namespace tq;
+  if (num_decode_seqs < 0 || num_prefill_seqs < 0 || num_q_rows < 0 || max_query_len < 0) {
+    take_timing_events();  // armed events apply to this call only
+    return TQ_ERR_INVALID_ARGUMENT;
+  }
+  // One side empty: the other side's own launch (and its own grid).
+  if (num_prefill_seqs == 0 || num_q_rows == 0 || max_query_len == 0)
+    return tq_paged_decode_write(dec_out, dec_out_row_stride, dec_q, dec_q_row_stride, k_new, k_new_row_stride,
+                                 v_new, v_new_row_stride, pool, num_blocks, num_layers, num_heads, block_size,
+                                 head_dim, layer, dec_block_tables, dec_block_table_stride, dec_max_blocks_per_seq,
+                                 context_lens, seq_order, num_decode_seqs, max_context_len, scale, partition_tokens,
+                                 workspace, workspace_bytes, d_error, stream);
+  if (num_decode_seqs == 0)
+    return tq_paged_prefill(pre_out, pre_out_row_stride, pre_q, pre_q_row_stride, pool, num_blocks, num_layers,
+                            num_heads, block_size, head_dim, layer, pre_block_tables, pre_block_table_stride,
+                            pre_max_blocks_per_seq, cu_seqlens_q, q_start, num_prefill_seqs, num_q_rows,
+                            max_query_len, scale, d_error, stream);
+
+  const TimingEvents timing = take_timing_events();  // for this call only, whatever it returns
+  if (k_new == nullptr || v_new == nullptr || pool == nullptr) return TQ_ERR_INVALID_ARGUMENT;
+  PrefillArgs pa;
+  bool empty;
+  tq_status st = make_prefill_args({pre_out, pre_out_row_stride, pre_q, pre_q_row_stride, pool, num_blocks,
+                                    num_layers, num_heads, block_size, head_dim, layer, pre_block_tables,
+                                    pre_block_table_stride, pre_max_blocks_per_seq, cu_seqlens_q, q_start,
+                                    num_prefill_seqs, num_q_rows, max_query_len, scale, d_error},
+                                   pa, empty);
+  if (st != TQ_OK) return st;
+  const int ks = choose_key_split((int64_t)pa.groups * pa.qtiles);
+  DecodeArgs da;
+  st = make_decode_args({dec_out, dec_out_row_stride, dec_q, dec_q_row_stride, k_new, k_new_row_stride, v_new,
+                         v_new_row_stride, pool, pool, num_blocks, num_layers, num_heads, block_size, head_dim, layer,
+                         dec_block_tables, dec_block_table_stride, dec_max_blocks_per_seq, context_lens, seq_order,
+                         num_decode_seqs, max_context_len, scale, partition_tokens, workspace, workspace_bytes,
+                         d_error},
+                        ks, da);
+  if (st != TQ_OK) return st;
+
+  // Decode units: (sequence, head) workgroups, or one wave per (sequence, head, partition).
+  const bool per_group = da.split_waves > 0;
+  const int64_t units = (int64_t)num_decode_seqs * num_heads * (per_group ? 1 : da.max_parts);
+  const int64_t groups = ((per_group ? units : (units + ks - 1) / ks) + kXcds - 1) / kXcds * kXcds;  // whole XCD rounds
+  if (units > 0x7fffffffLL || groups + pa.total > 0x7fffffffLL) return TQ_ERR_UNSUPPORTED;
+  const bool merge = !per_group && da.max_parts > 1;
+  hipStream_t s = (hipStream_t)stream;
+  const int32_t g32 = (int32_t)groups, u32 = (int32_t)units;
+  hipEvent_t stop = merge ? nullptr : timing.stop;
+  switch (block_size) {
+    case 16: launch_mixed<16, 16>(pa, da, ks, g32, u32, s, timing.start, stop); break;
+    case 32: launch_mixed<32, 0>(pa, da, ks, g32, u32, s, timing.start, stop); break;
+    default: launch_mixed<0, 0>(pa, da, ks, g32, u32, s, timing.start, stop); break;
+  }
+  if (merge) launch_decode_merge(da, num_decode_seqs, s, timing.stop);
   return check_launch();
 }

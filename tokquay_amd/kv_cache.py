@@ -183,9 +183,13 @@ class PagedBatch(BatchedKV):
     flat ``[B * T]`` padded input, ``last_rows`` gives each sequence's last row.
     """
 
-    # Optional callable(batch, kind) run right before every decode ("decode") and prefill
-    # ("prefill") attention launch; a benchmark uses it to arm launch-recorded timing events.
+    # Optional callable(batch, kind) run right before every decode ("decode"), prefill
+    # ("prefill") and mixed ("mixed") attention launch; a benchmark uses it to arm
+    # launch-recorded timing events.
     launch_hook = None
+    # A step holding both decode and prefill rows runs their attention as one launch
+    # (tq_paged_mixed); False keeps two launches, decode then prefill (for comparison).
+    one_launch_mixed = True
 
     def __init__(
         self,
@@ -237,6 +241,7 @@ class PagedBatch(BatchedKV):
                      Bd * nbd + Bd + Bp * nbp + 2 * Bp + 1)  # fmt: skip
         self._workspace: torch.Tensor | None = None
         self._ws_bytes = 0
+        self._ws_mixed = False  # the workspace was sized for the one-launch mixed grid
         self._lazy: dict[str, torch.Tensor] = {}
 
     # ---- device metadata views (sections of the two packed buffers) ----
@@ -353,9 +358,11 @@ class PagedBatch(BatchedKV):
         Launches, all on the current stream: decode attention for the one-token rows
         with their cache write folded in (``tq_paged_decode_write``), then - for the
         rows of sequences feeding several tokens - their cache write and prefill
-        attention. One call into the native extension makes all of them; with a
-        ``launch_hook`` set they go one by one through ctypes, the hook before each
-        attention kernel.
+        attention. When both kinds of row are present the two attention launches are
+        one (``tq_paged_mixed``, after the prefill rows' cache write) unless
+        ``one_launch_mixed`` is off. One call into the native extension makes all of
+        them; with a ``launch_hook`` set they go one by one through ctypes, the hook
+        before each attention kernel.
         """
         pool = self.pool
         nb, n_layer, _, n_head, bs, d = pool.shape
@@ -375,9 +382,15 @@ class PagedBatch(BatchedKV):
         qp, pp, op = qkv.data_ptr(), pool.data_ptr(), out.data_ptr()
         scale = 1.0 / math.sqrt(d)
         Bd, Bp = self.num_decode, self.num_prefill
-        if Bd and self._workspace is None:
-            self._ws_bytes = int(L.tq_paged_decode_workspace_size(Bd, n_head, d, self.decode_max_ctx, self.partition_tokens))
+        mixed = bool(Bd and Bp and PagedBatch.one_launch_mixed)
+        if Bd and (self._workspace is None or self._ws_mixed != mixed):
+            if mixed:
+                self._ws_bytes = int(L.tq_paged_mixed_workspace_size(Bd, n_head, d, self.decode_max_ctx, self.partition_tokens,
+                                                                     Bp, N - Bd, self.prefill_max_q))  # fmt: skip
+            else:
+                self._ws_bytes = int(L.tq_paged_decode_workspace_size(Bd, n_head, d, self.decode_max_ctx, self.partition_tokens))
             self._workspace = torch.empty(max(self._ws_bytes, 1), dtype=torch.uint8, device=pool.device)
+            self._ws_mixed = mixed
         ws = self._workspace.data_ptr() if Bd else 0
         slots = self._d64.data_ptr() + 8 * 2 * N
 
@@ -386,11 +399,49 @@ class PagedBatch(BatchedKV):
                 op, qp, pp, nb, n_layer, n_head, bs, d, layer, scale, stream, err or 0, N,
                 Bd, self._ptr32(0), self._nbd, self._ptr32(1), self._ptr32(5), self.decode_max_ctx,
                 self.partition_tokens, ws, self._ws_bytes,
-                Bp, slots, self._ptr32(2), self._nbp, self._ptr32(3), self._ptr32(4), self.prefill_max_q,
+                Bp, slots, self._ptr32(2), self._nbp, self._ptr32(3), self._ptr32(4), self.prefill_max_q, int(mixed),
             )  # fmt: skip
             if failed is not None:
                 _lib.check(*failed)
             return out
+
+        # Per-kernel launches, with the hook armed before each attention kernel.
+        off = Bd * row3 * 4  # bytes to the first prefill row of qkv
+        if Bp:
+            _lib.check(
+                L.tq_cache_write(pp, nb, n_layer, n_head, bs, d, layer, qp + off + 4 * C, row3, qp + off + 8 * C,
+                                 row3, slots + 8 * Bd, N - Bd, err, stream),
+                "tq_cache_write",
+            )  # fmt: skip
+        if mixed:
+            PagedBatch.launch_hook(self, "mixed")
+            _lib.check(
+                L.tq_paged_mixed(op, C, qp, row3, qp + 4 * C, row3, qp + 8 * C, row3, self._ptr32(0), self._nbd,
+                                 self._nbd, self._ptr32(1), self._ptr32(5), Bd, self.decode_max_ctx,
+                                 self.partition_tokens, op + 4 * Bd * C, C, qp + off, row3, self._ptr32(2), self._nbp,
+                                 self._nbp, self._ptr32(3), self._ptr32(4), Bp, N - Bd, self.prefill_max_q, pp, nb,
+                                 n_layer, n_head, bs, d, layer, scale, ws, self._ws_bytes, err, stream),
+                "tq_paged_mixed",
+            )  # fmt: skip
+            return out
+        if Bd:
+            PagedBatch.launch_hook(self, "decode")
+            _lib.check(
+                L.tq_paged_decode_write(op, C, qp, row3, qp + 4 * C, row3, qp + 8 * C, row3, pp, nb, n_layer,
+                                        n_head, bs, d, layer, self._ptr32(0), self._nbd, self._nbd, self._ptr32(1),
+                                        self._ptr32(5), Bd, self.decode_max_ctx, scale, self.partition_tokens, ws,
+                                        self._ws_bytes, err, stream),
+                "tq_paged_decode_write",
+            )  # fmt: skip
+        if Bp:
+            PagedBatch.launch_hook(self, "prefill")
+            _lib.check(
+                L.tq_paged_prefill(op + 4 * Bd * C, C, qp + off, row3, pp, nb, n_layer, n_head, bs, d, layer,
+                                   self._ptr32(2), self._nbp, self._nbp, self._ptr32(3), self._ptr32(4), Bp, N - Bd,
+                                   self.prefill_max_q, scale, err, stream),
+                "tq_paged_prefill",
+            )  # fmt: skip
+        return out
 
         # Per-kernel launches, with the hook armed before each attention kernel.
         if Bd:

@@ -195,6 +195,91 @@ def paged_prefill(
     _lib.check(st, "tq_paged_prefill")
 
 
+def _tables(t: torch.Tensor, name: str, n: int, device: torch.device) -> int:
+    """Validates an int32 [B, max_blocks] block-table tensor and returns its row stride."""
+    if t.dtype != torch.int32 or t.device != device or t.dim() != 2:
+        raise ValueError(f"{name} must be an int32 [B, max_blocks] tensor on the pool's device")
+    if t.size(0) != n or (t.size(1) > 1 and t.stride(1) != 1):
+        raise ValueError(f"{name} must have one row per sequence with contiguous rows")
+    return t.stride(0) if n > 1 else t.size(1)
+
+
+def mixed_workspace_bytes(num_decode: int, n_head: int, max_context_len: int, partition_tokens: int,
+                          num_prefill: int, num_q_rows: int, max_query_len: int) -> int:  # fmt: skip
+    return int(_lib.lib().tq_paged_mixed_workspace_size(num_decode, n_head, HEAD_DIM, max_context_len, partition_tokens,
+                                                        num_prefill, num_q_rows, max_query_len))  # fmt: skip
+
+
+def paged_mixed(
+    dec_out: torch.Tensor,
+    dec_q: torch.Tensor,
+    k_new: torch.Tensor,
+    v_new: torch.Tensor,
+    dec_block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    max_context_len: int,
+    pre_out: torch.Tensor,
+    pre_q: torch.Tensor,
+    pre_block_tables: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    q_start: torch.Tensor,
+    max_query_len: int,
+    pool: torch.Tensor,
+    layer: int,
+    scale: float | None = None,
+    partition_tokens: int = 0,
+    workspace: torch.Tensor | None = None,
+    d_error: torch.Tensor | None = None,
+    seq_order: torch.Tensor | None = None,
+) -> None:
+    """One launch for a step's decode rows (``paged_decode`` with ``k_new`` / ``v_new``: their new K/V
+    written, then one query each over its context) and its prefill rows (``paged_prefill``; their
+    K/V must already be in the pool). Each output row is bit-identical to the single-kind call's
+    (decode rows: at the same explicit ``partition_tokens``)."""
+    nb, n_layer, n_head, bs, d = _pool_dims(pool)
+    if not 0 <= layer < n_layer:
+        raise ValueError(f"layer {layer} out of range [0, {n_layer})")
+    nd = context_lens.numel()
+    _int_tensor(context_lens, "context_lens", torch.int32, pool.device)
+    dbt = _tables(dec_block_tables, "dec_block_tables", nd, pool.device)
+    dqs = _rows(dec_q, "dec_q", nd, n_head, pool.device)
+    dos = _rows(dec_out, "dec_out", nd, n_head, pool.device)
+    ks = _rows(k_new, "k_new", nd, n_head, pool.device)
+    vs = _rows(v_new, "v_new", nd, n_head, pool.device)
+    _int_tensor(cu_seqlens_q, "cu_seqlens_q", torch.int32, pool.device)
+    _int_tensor(q_start, "q_start", torch.int32, pool.device)
+    npf = q_start.numel()
+    if cu_seqlens_q.numel() != npf + 1:
+        raise ValueError("cu_seqlens_q must have num_prefill_seqs + 1 entries")
+    pbt = _tables(pre_block_tables, "pre_block_tables", npf, pool.device)
+    n_rows = pre_q.size(0)
+    pqs = _rows(pre_q, "pre_q", n_rows, n_head, pool.device)
+    pos = _rows(pre_out, "pre_out", n_rows, n_head, pool.device)
+    order = None
+    if seq_order is not None:
+        _int_tensor(seq_order, "seq_order", torch.int32, pool.device)
+        if seq_order.numel() != nd:
+            raise ValueError(f"seq_order needs {nd} entries")
+        order = seq_order.data_ptr()
+    scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
+    need = mixed_workspace_bytes(nd, n_head, max_context_len, partition_tokens, npf, n_rows, max_query_len) if nd else 0
+    ws_ptr, ws_bytes = None, 0
+    if need:
+        if workspace is None:
+            workspace = torch.empty(need, dtype=torch.uint8, device=pool.device)
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    err = d_error.data_ptr() if d_error is not None else None
+    st = _lib.lib().tq_paged_mixed(
+        dec_out.data_ptr(), dos, dec_q.data_ptr(), dqs, k_new.data_ptr(), ks, v_new.data_ptr(), vs,
+        dec_block_tables.data_ptr(), dbt, dec_block_tables.size(1), context_lens.data_ptr(), order, nd,
+        int(max_context_len), partition_tokens,
+        pre_out.data_ptr(), pos, pre_q.data_ptr(), pqs, pre_block_tables.data_ptr(), pbt, pre_block_tables.size(1),
+        cu_seqlens_q.data_ptr(), q_start.data_ptr(), npf, n_rows, int(max_query_len),
+        pool.data_ptr(), nb, n_layer, n_head, bs, d, layer, scale, ws_ptr, ws_bytes, err, _stream(pool.device),
+    )  # fmt: skip
+    _lib.check(st, "tq_paged_mixed")
+
+
 def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """Greedy ids ``[R]`` (int64) of float32 logits ``[R, V]``: the reference's ``logits.argmax(-1)``
     (tokquay/engine.py:190) - the lowest index of each row's maximum, NaN above every number."""
