@@ -17,9 +17,11 @@ them:
   torch, on the same GPU, from the same state, with greedy-id agreement;
 * ``decode_op_alone``: the decode kernel alone on the 64-sequence op shape;
 * ``prefill``: the prefill kernel's fp32 MFMA utilisation over mixed
-  chunked-prefill + decode steps, and ``mixed_engine``: the same scenario
-  through ``Engine.step`` with chunked prefill and with the reference's
-  alternating policy;
+  chunked-prefill + decode steps; ``mixed_attention``: the same steps' attention
+  as one launch per layer for both kinds of row (its combined HBM + MFMA
+  roofline, against two launches); ``mixed_engine``: the same scenario through
+  ``Engine.step`` with chunked prefill and with the reference's alternating
+  policy;
 * ``itl`` / ``itl_chunked`` / ``saturated``: the 300-request serving trace
   (p50 / p99 inter-token latency) with each policy, and all requests at t=0.
 
@@ -83,35 +85,41 @@ def prefill_flops(starts: list[int], lens: list[int], n_head: int = N_HEAD, d: i
 
 
 class LaunchTimer:
-    """Times every attention launch of one kind ("decode" or "prefill") with HIP events that the
-    launch itself records at the start and end of its kernels (tq_set_timing_events)."""
+    """Times attention launches per kind - "decode", "prefill", or "mixed" (both kinds of row in one
+    tq_paged_mixed launch) - with HIP events that the launch itself records at the start and end of
+    its kernels (tq_set_timing_events), and adds up each kind's algorithmic decode bytes and prefill
+    flops."""
 
-    def __init__(self, kind: str):
+    def __init__(self, *kinds: str):
         import torch
 
         from tokquay_amd import _lib
 
-        self.torch, self.lib, self.kind = torch, _lib.lib(), kind
-        self.pairs = []
-        self.bytes = 0
-        self.flops = 0
+        self.torch, self.lib = torch, _lib.lib()
+        self.pairs = {k: [] for k in kinds}
+        self.bytes = dict.fromkeys(kinds, 0)
+        self.flops = dict.fromkeys(kinds, 0)
 
     def __call__(self, batch, kind):
-        if kind != self.kind:
+        if kind not in self.pairs:
             return
         start, stop = self.torch.cuda.Event(enable_timing=True), self.torch.cuda.Event(enable_timing=True)
         start.record()  # creates the events; the kernel launch records them again at its own start / end
         stop.record()
         self.lib.tq_set_timing_events(start.cuda_event, stop.cuda_event)
-        self.pairs.append((start, stop))
-        rows = [b for b in range(batch.B) if (batch.new_lens[b] == 1) == (kind == "decode")]
-        if kind == "decode":
-            self.bytes += decode_bytes([batch.context_lens[b] for b in rows])
-        else:
-            self.flops += prefill_flops([batch.start[b] for b in rows], [batch.new_lens[b] for b in rows])
+        self.pairs[kind].append((start, stop))
+        dec = [b for b in range(batch.B) if batch.new_lens[b] == 1]
+        pre = [b for b in range(batch.B) if batch.new_lens[b] != 1]
+        if kind in ("decode", "mixed"):
+            self.bytes[kind] += decode_bytes([batch.context_lens[b] for b in dec])
+        if kind in ("prefill", "mixed"):
+            self.flops[kind] += prefill_flops([batch.start[b] for b in pre], [batch.new_lens[b] for b in pre])
 
-    def total_ms(self) -> float:
-        return sum(a.elapsed_time(b) for a, b in self.pairs)
+    def launches(self, kind: str) -> int:
+        return len(self.pairs[kind])
+
+    def total_ms(self, kind: str) -> float:
+        return sum(a.elapsed_time(b) for a, b in self.pairs[kind])
 
 
 def load_model(seed: int = 0):
@@ -229,10 +237,14 @@ def decode_op_alone(seed: int = 2) -> dict:
             "achieved_GBs": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}  # fmt: skip
 
 
-def mixed_chunked_step(seed: int = 5) -> dict:
+def mixed_chunked_step(seed: int = 5) -> tuple[dict, dict]:
     """Mixed chunked-prefill + decode steps: 4 prompts of U[512,1024] random tokens fed in 256-token
     chunks (chunk k starts at 256k) next to 128 sequences decoding at context U[64,768], block size 16.
-    Reports the prefill kernel's MFMA utilisation (causal-exact flops / launch time / fp32 peak)."""
+    Each chunk step runs twice from the same state: with the step's attention as two launches per
+    layer (decode rows, then prefill rows; each timed) and as one tq_paged_mixed launch. Returns the
+    prefill kernel's fp32 MFMA utilisation (causal-exact flops / launch time / peak) in the two-launch
+    runs, and the one launch's combined roofline: the time the decode rows' bytes take at HBM peak
+    plus the time the prefill flops take at MFMA peak, over the measured launch time."""
     import torch
 
     from tokquay_amd import kv_cache
@@ -252,36 +264,63 @@ def mixed_chunked_step(seed: int = 5) -> dict:
         for s, t in zip(decoders[i : i + 32], nxt):
             s.append_token(t)
             alloc.append_slot(s)
-    chunks = []
-    for k in range(4):
-        live = [p for p in prompts if p.num_cached_tokens < p.num_tokens]
-        seqs = live + decoders
-        lens = [min(256, p.num_tokens - p.num_cached_tokens) for p in live] + [1] * len(decoders)
-        starts = [p.num_cached_tokens for p in live]
-        timer = LaunchTimer("prefill")
-        kv_cache.PagedBatch.launch_hook = timer
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        nxt = paged_forward(model, alloc, seqs, lens).argmax(-1).tolist()
-        torch.cuda.synchronize()
-        step_ms = (time.perf_counter() - t0) * 1e3
+    chunks, mixed = [], []
+    same = compared = 0
+    max_diff = 0.0
+    try:
+        for k in range(4):
+            live = [p for p in prompts if p.num_cached_tokens < p.num_tokens]
+            seqs = live + decoders
+            lens = [min(256, p.num_tokens - p.num_cached_tokens) for p in live] + [1] * len(decoders)
+            starts = [p.num_cached_tokens for p in live]
+            cached = [s.num_cached_tokens for s in seqs]
+            runs = {}
+            for one in (False, True):  # the same step from the same state (the K/V it writes are the same)
+                for s, c in zip(seqs, cached):
+                    s.num_cached_tokens = c
+                kv_cache.PagedBatch.one_launch_mixed = one
+                timer = LaunchTimer("decode", "prefill", "mixed")
+                kv_cache.PagedBatch.launch_hook = timer
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                logits = paged_forward(model, alloc, seqs, lens)
+                torch.cuda.synchronize()
+                runs[one] = (timer, logits, (time.perf_counter() - t0) * 1e3)
+                kv_cache.PagedBatch.launch_hook = None
+            two, one = runs[False][0], runs[True][0]
+            ids_two, ids_one = runs[False][1].argmax(-1).tolist(), runs[True][1].argmax(-1).tolist()
+            same += sum(a == b for a, b in zip(ids_two, ids_one))
+            compared += len(ids_one)
+            max_diff = max(max_diff, float((runs[False][1] - runs[True][1]).abs().max()))
+            for s, t in zip(decoders, ids_one[len(live) :]):
+                s.append_token(t)
+                alloc.append_slot(s)
+            n = two.launches("prefill")
+            pre_us = two.total_ms("prefill") / n * 1e3
+            dec_us = two.total_ms("decode") / two.launches("decode") * 1e3
+            mix_us = one.total_ms("mixed") / one.launches("mixed") * 1e3
+            flops = two.flops["prefill"] / n
+            nbytes = one.bytes["mixed"] / one.launches("mixed")
+            ideal_us = nbytes / (HBM_PEAK_GBS * 1e3) + flops / (MFMA_FP32_PEAK_TFLOPS * 1e6)
+            chunks.append({"chunk": k, "prompt_rows": len(live), "starts": starts, "prefill_us": round(pre_us, 2),
+                           "mflop_per_launch": round(flops / 1e6, 1), "tflops": round(flops / pre_us / 1e6, 2),
+                           "frac": round(flops / pre_us / 1e6 / MFMA_FP32_PEAK_TFLOPS, 4),
+                           "step_ms": round(runs[False][2], 3)})  # fmt: skip
+            mixed.append({"chunk": k, "decode_mb": round(nbytes / 1e6, 1), "prefill_mflop": round(flops / 1e6, 1),
+                          "ideal_us": round(ideal_us, 2), "one_launch_us": round(mix_us, 2),
+                          "two_launch_us": round(dec_us + pre_us, 2), "decode_us": round(dec_us, 2),
+                          "frac": round(ideal_us / mix_us, 4), "two_launch_frac": round(ideal_us / (dec_us + pre_us), 4),
+                          "step_ms": round(runs[True][2], 3)})  # fmt: skip
+    finally:
+        kv_cache.PagedBatch.one_launch_mixed = True
         kv_cache.PagedBatch.launch_hook = None
-        for s, t in zip(decoders, nxt[len(live) :]):
-            s.append_token(t)
-            alloc.append_slot(s)
-        if not timer.pairs:
-            continue
-        us = timer.total_ms() / len(timer.pairs) * 1e3
-        flops = timer.flops / len(timer.pairs)
-        chunks.append({"chunk": k, "prompt_rows": len(live), "starts": starts, "prefill_us": round(us, 2),
-                       "mflop_per_launch": round(flops / 1e6, 1), "tflops": round(flops / us / 1e6, 2),
-                       "frac": round(flops / us / 1e6 / MFMA_FP32_PEAK_TFLOPS, 4), "step_ms": round(step_ms, 3)})  # fmt: skip
     alloc.check_device_errors()
+    workload = "4 prompts U[512,1024] in 256-token chunks + 128 decoding sequences, ctx U[64,768], block 16"
     tot_f = sum(c["mflop_per_launch"] for c in chunks)
     tot_us = sum(c["prefill_us"] for c in chunks)
-    return {
-        "workload": "4 prompts U[512,1024] in 256-token chunks + 128 decoding sequences, ctx U[64,768], block 16",
-        "kernel": "tq_paged_prefill (fp32 MFMA 16x16x4)",
+    prefill = {
+        "workload": workload,
+        "kernel": "tq_paged_prefill (fp32 MFMA 16x16x4), launched on its own",
         "bound": "mfma",
         "achieved": round(tot_f / tot_us, 2),
         "peak": MFMA_FP32_PEAK_TFLOPS,
@@ -289,6 +328,24 @@ def mixed_chunked_step(seed: int = 5) -> dict:
         "frac": round(tot_f / tot_us / MFMA_FP32_PEAK_TFLOPS, 4),
         "chunks": chunks,
     }
+    ideal = sum(m["ideal_us"] for m in mixed)
+    one_us = sum(m["one_launch_us"] for m in mixed)
+    two_us = sum(m["two_launch_us"] for m in mixed)
+    mixed_attention = {
+        "workload": workload,
+        "kernel": "tq_paged_mixed (decode rows and prefill tiles in one launch per layer)",
+        "bound": "hbm + mfma: decode bytes at 8 TB/s plus prefill flops at 157.3 TFLOP/s",
+        "ideal_us": round(ideal, 2),
+        "one_launch_us": round(one_us, 2),
+        "frac": round(ideal / one_us, 4),
+        "two_launch_us": round(two_us, 2),
+        "two_launch_frac": round(ideal / two_us, 4),
+        "speedup_over_two_launches": round(two_us / one_us, 3),
+        "greedy_ids_vs_two_launches": {"ids_compared": compared, "ids_identical": same,
+                                       "max_abs_logit_diff": max_diff},  # fmt: skip
+        "chunks": mixed,
+    }
+    return prefill, mixed_attention
 
 
 def mixed_engine(chunked: bool, seed: int = 5) -> dict:
@@ -651,8 +708,8 @@ def main() -> int:
     ap.add_argument("--configs", action="store_true",
                     help="only run the small configurations beside the gather path (GPU and CPU) and exit")
     ap.add_argument("--pmc-probe", action="store_true",
-                    help="run 3 copies of a known size (1 GiB read + 1 GiB write) and 3 decode steps, then exit; "
-                    "for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")  # fmt: skip
+                    help="run 3 copies of a known size (1 GiB read + 1 GiB write), 3 decode steps and the mixed "
+                    "chunked-prefill steps, then exit; for rocprofv3 --pmc runs")  # fmt: skip
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path.", file=sys.stderr)
@@ -690,8 +747,13 @@ def main() -> int:
         for _ in range(3):
             engine.step()
         torch.cuda.synchronize()
-        print(json.dumps({"pmc_probe": True, "copy_bytes": x.numel() * 4,
-                          "decode_bytes_first_step": decode_bytes(first_ctx)}), flush=True)  # fmt: skip
+        del engine, x, y
+        torch.cuda.empty_cache()
+        _, mixed = mixed_chunked_step()  # config 5's chunk steps, as two launches and as one
+        print(json.dumps({"pmc_probe": True, "copy_bytes": 1 << 30,
+                          "decode_bytes_first_step": decode_bytes(first_ctx),
+                          "mixed_chunks": [{k: c[k] for k in ("chunk", "prefill_mflop", "decode_mb")} for c in mixed["chunks"]]}),
+              flush=True)  # fmt: skip
         return 0
     running = list(engine.scheduler.running)
     assert len(running) == N_SEQS, f"{len(running)} sequences running, expected {N_SEQS}"
@@ -751,9 +813,9 @@ def main() -> int:
     kv_cache.PagedBatch.launch_hook = None
     engine.graphs = graphs
     engine.allocator.check_device_errors()
-    n_launch = len(timer.pairs)
-    kern_ms = timer.total_ms() / n_launch
-    bytes_per_launch = timer.bytes / n_launch
+    n_launch = timer.launches("decode")
+    kern_ms = timer.total_ms("decode") / n_launch
+    bytes_per_launch = timer.bytes["decode"] / n_launch
     achieved = bytes_per_launch / (kern_ms * 1e-3) / 1e9
     log(f"decode (graph replay): {ms_per_step:.3f} ms/step, {tok_s:.0f} tok/s; kernel-timing eager steps "
         f"{eager_ms:.3f} ms/step (every decode launch timed on its own); "
@@ -832,8 +894,10 @@ def main() -> int:
     result["decode_op_alone"] = decode_op_alone()
     if not args.no_prefill:
         log("mixed chunked-prefill + decode steps ...")
-        result["prefill"] = mixed_chunked_step()
-        log(f"prefill: {result['prefill']['achieved']} TFLOP/s = {result['prefill']['frac']:.3f} of fp32 MFMA peak")
+        result["prefill"], result["mixed_attention"] = mixed_chunked_step()
+        log(f"prefill: {result['prefill']['achieved']} TFLOP/s = {result['prefill']['frac']:.3f} of fp32 MFMA peak; "
+            f"mixed launch: {result['mixed_attention']['frac']:.3f} of its combined roofline "
+            f"({result['mixed_attention']['two_launch_frac']:.3f} as two launches)")
         result["mixed_engine"] = [mixed_engine(chunked=True), mixed_engine(chunked=False)]
         torch.cuda.empty_cache()
     if not args.no_itl:
