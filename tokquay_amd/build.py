@@ -26,6 +26,9 @@ LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 OFFLOAD_ARCH = "gfx950"
 NATIVE_SRC = os.path.join(CSRC_DIR, "native.cpp")
 NATIVE_PATH = os.path.join(PKG_DIR, "_native" + sysconfig.get_config_var("EXT_SUFFIX"))
+TORCH_OPS_SRC = os.path.join(CSRC_DIR, "torch_ops.cpp")
+TORCH_OPS_PATH = os.path.join(PKG_DIR, "_torch_ops.so")
+ROCM_INCLUDE = "/opt/rocm/include"
 
 HIPCC_FLAGS = [
     f"--offload-arch={OFFLOAD_ARCH}",
@@ -48,6 +51,7 @@ HIPCC_FLAGS = [
 
 
 def sources() -> list[str]:
+    """The kernel sources (every ``*.hip`` under ``csrc``)."""
     return sorted(os.path.join(CSRC_DIR, f) for f in os.listdir(CSRC_DIR) if f.endswith(".hip"))
 
 
@@ -59,9 +63,11 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = False) -> str:
-    """Compile every kernel source into LIB_PATH, then the ``_native`` extension; return LIB_PATH."""
+    """Compile every kernel source into LIB_PATH, then the ``_native`` extension and the torch
+    operator library; return LIB_PATH."""
     build_kernels(verbose)
     build_native(verbose)
+    build_torch_ops(verbose)
     return LIB_PATH
 
 
@@ -101,6 +107,33 @@ def build_native(verbose: bool = False) -> str:
         print(proc.stdout + proc.stderr, flush=True)
     os.replace(tmp, NATIVE_PATH)
     return NATIVE_PATH
+
+
+def build_torch_ops(verbose: bool = False) -> str:
+    """Compile ``csrc/torch_ops.cpp`` (the entry points registered as ``torch.ops.tokquay_amd.*``)
+    against torch's headers and libraries; it links LIB_PATH. Returns its path."""
+    import torch
+    from torch.utils import cpp_extension
+
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if cxx is None:
+        raise RuntimeError("no host C++ compiler (g++) found")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    torch_lib = cpp_extension.library_paths()[0]
+    tmp = TORCH_OPS_PATH + ".tmp"
+    # torch's HIP stream header includes the HIP runtime's, which needs the platform named when the
+    # host compiler is not hipcc.
+    cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           "-D__HIP_PLATFORM_AMD__=1", *[f"-I{p}" for p in cpp_extension.include_paths()], f"-I{ROCM_INCLUDE}",
+           f"-I{INCLUDE_DIR}", "-o", tmp, TORCH_OPS_SRC, f"-L{PKG_DIR}", "-l:" + LIB_NAME, f"-L{torch_lib}",
+           "-lc10", "-lc10_hip", "-ltorch_cpu", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}"]  # fmt: skip
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"{cxx} failed ({proc.returncode}):\n{proc.stdout}{proc.stderr}")
+    os.replace(tmp, TORCH_OPS_PATH)
+    return TORCH_OPS_PATH
 
 
 if __name__ == "__main__":

@@ -20,9 +20,20 @@ import math
 
 import torch
 
-from tokquay_amd import _lib
+from tokquay_amd import _lib, torch_ops
 
 HEAD_DIM = 64
+
+
+def _op(name: str, *args) -> None:
+    """Calls ``torch.ops.tokquay_amd.<name>``; a failed C-ABI status raises ``_lib.KernelError``."""
+    try:
+        getattr(torch_ops.load(), name)(*args)
+    except RuntimeError as e:
+        first = str(e).splitlines()[0] if str(e) else ""
+        if " failed: " in first and first.startswith("tq_"):
+            raise _lib.KernelError(first) from None
+        raise
 
 
 def _stream(device: torch.device) -> int:
@@ -76,14 +87,9 @@ def cache_write(
         raise ValueError(f"layer {layer} out of range [0, {n_layer})")
     n = slot_mapping.numel()
     _int_tensor(slot_mapping, "slot_mapping", torch.int64, pool.device)
-    ks = _rows(k, "k", n, n_head, pool.device)
-    vs = _rows(v, "v", n, n_head, pool.device)
-    err = d_error.data_ptr() if d_error is not None else None
-    st = _lib.lib().tq_cache_write(
-        pool.data_ptr(), nb, n_layer, n_head, bs, d, layer,
-        k.data_ptr(), ks, v.data_ptr(), vs, slot_mapping.data_ptr(), n, err, _stream(pool.device),
-    )  # fmt: skip
-    _lib.check(st, "tq_cache_write")
+    _rows(k, "k", n, n_head, pool.device)
+    _rows(v, "v", n, n_head, pool.device)
+    _op("cache_write", pool, layer, k, v, slot_mapping, d_error)
 
 
 def decode_workspace_bytes(num_seqs: int, n_head: int, max_context_len: int, partition_tokens: int = 0) -> int:
@@ -121,37 +127,28 @@ def paged_decode(
         raise ValueError("block_tables must be an int32 [B, max_blocks] tensor on the pool's device")
     if block_tables.size(0) != n or (block_tables.size(1) > 1 and block_tables.stride(1) != 1):
         raise ValueError("block_tables must have one row per sequence with contiguous rows")
-    qs = _rows(q, "q", n, n_head, pool.device)
-    os_ = _rows(out, "out", n, n_head, pool.device)
+    _rows(q, "q", n, n_head, pool.device)
+    _rows(out, "out", n, n_head, pool.device)
     scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
     need = decode_workspace_bytes(n, n_head, max_context_len, partition_tokens) if n else 0
-    ws_ptr, ws_bytes = None, 0
-    if need:
-        if workspace is None:
-            workspace = torch.empty(need, dtype=torch.uint8, device=pool.device)
-        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
-    err = d_error.data_ptr() if d_error is not None else None
-    bt_stride = block_tables.stride(0) if n > 1 else block_tables.size(1)
-    order = None
+    if need and workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=pool.device)
+    if not need:
+        workspace = None
     if seq_order is not None:
         _int_tensor(seq_order, "seq_order", torch.int32, pool.device)
         if seq_order.numel() != n:
             raise ValueError(f"seq_order needs {n} entries")
-        order = seq_order.data_ptr()
-    tail = (pool.data_ptr(), nb, n_layer, n_head, bs, d, layer, block_tables.data_ptr(), bt_stride,
-            block_tables.size(1), context_lens.data_ptr(), order, n, int(max_context_len), scale, partition_tokens,
-            ws_ptr, ws_bytes, err, _stream(pool.device))  # fmt: skip
+    tail = (layer, block_tables, context_lens, int(max_context_len), scale, partition_tokens, workspace, d_error,
+            seq_order)  # fmt: skip
     if k_new is None and v_new is None:
-        st = _lib.lib().tq_paged_decode(out.data_ptr(), os_, q.data_ptr(), qs, *tail)
-        _lib.check(st, "tq_paged_decode")
+        _op("paged_decode", out, q, pool, *tail)
         return
     if k_new is None or v_new is None:
         raise ValueError("k_new and v_new go together")
-    ks = _rows(k_new, "k_new", n, n_head, pool.device)
-    vs = _rows(v_new, "v_new", n, n_head, pool.device)
-    st = _lib.lib().tq_paged_decode_write(out.data_ptr(), os_, q.data_ptr(), qs, k_new.data_ptr(), ks,
-                                          v_new.data_ptr(), vs, *tail)  # fmt: skip
-    _lib.check(st, "tq_paged_decode_write")
+    _rows(k_new, "k_new", n, n_head, pool.device)
+    _rows(v_new, "v_new", n, n_head, pool.device)
+    _op("paged_decode_write", out, q, k_new, v_new, pool, *tail)
 
 
 def paged_prefill(
@@ -181,18 +178,10 @@ def paged_prefill(
     if block_tables.size(0) != n_seq or (block_tables.size(1) > 1 and block_tables.stride(1) != 1):
         raise ValueError("block_tables must have one row per sequence with contiguous rows")
     n_rows = q.size(0)
-    qs = _rows(q, "q", n_rows, n_head, pool.device)
-    os_ = _rows(out, "out", n_rows, n_head, pool.device)
+    _rows(q, "q", n_rows, n_head, pool.device)
+    _rows(out, "out", n_rows, n_head, pool.device)
     scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
-    err = d_error.data_ptr() if d_error is not None else None
-    bt_stride = block_tables.stride(0) if n_seq > 1 else block_tables.size(1)
-    st = _lib.lib().tq_paged_prefill(
-        out.data_ptr(), os_, q.data_ptr(), qs, pool.data_ptr(), nb, n_layer, n_head, bs, d, layer,
-        block_tables.data_ptr(), bt_stride, block_tables.size(1),
-        cu_seqlens_q.data_ptr(), q_start.data_ptr(), n_seq, n_rows, int(max_query_len), scale,
-        err, _stream(pool.device),
-    )  # fmt: skip
-    _lib.check(st, "tq_paged_prefill")
+    _op("paged_prefill", out, q, pool, layer, block_tables, cu_seqlens_q, q_start, int(max_query_len), scale, d_error)
 
 
 def _tables(t: torch.Tensor, name: str, n: int, device: torch.device) -> int:
@@ -241,43 +230,31 @@ def paged_mixed(
         raise ValueError(f"layer {layer} out of range [0, {n_layer})")
     nd = context_lens.numel()
     _int_tensor(context_lens, "context_lens", torch.int32, pool.device)
-    dbt = _tables(dec_block_tables, "dec_block_tables", nd, pool.device)
-    dqs = _rows(dec_q, "dec_q", nd, n_head, pool.device)
-    dos = _rows(dec_out, "dec_out", nd, n_head, pool.device)
-    ks = _rows(k_new, "k_new", nd, n_head, pool.device)
-    vs = _rows(v_new, "v_new", nd, n_head, pool.device)
+    _tables(dec_block_tables, "dec_block_tables", nd, pool.device)
+    for t, name in ((dec_q, "dec_q"), (dec_out, "dec_out"), (k_new, "k_new"), (v_new, "v_new")):
+        _rows(t, name, nd, n_head, pool.device)
     _int_tensor(cu_seqlens_q, "cu_seqlens_q", torch.int32, pool.device)
     _int_tensor(q_start, "q_start", torch.int32, pool.device)
     npf = q_start.numel()
     if cu_seqlens_q.numel() != npf + 1:
         raise ValueError("cu_seqlens_q must have num_prefill_seqs + 1 entries")
-    pbt = _tables(pre_block_tables, "pre_block_tables", npf, pool.device)
+    _tables(pre_block_tables, "pre_block_tables", npf, pool.device)
     n_rows = pre_q.size(0)
-    pqs = _rows(pre_q, "pre_q", n_rows, n_head, pool.device)
-    pos = _rows(pre_out, "pre_out", n_rows, n_head, pool.device)
-    order = None
+    _rows(pre_q, "pre_q", n_rows, n_head, pool.device)
+    _rows(pre_out, "pre_out", n_rows, n_head, pool.device)
     if seq_order is not None:
         _int_tensor(seq_order, "seq_order", torch.int32, pool.device)
         if seq_order.numel() != nd:
             raise ValueError(f"seq_order needs {nd} entries")
-        order = seq_order.data_ptr()
     scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
     need = mixed_workspace_bytes(nd, n_head, max_context_len, partition_tokens, npf, n_rows, max_query_len) if nd else 0
-    ws_ptr, ws_bytes = None, 0
-    if need:
-        if workspace is None:
-            workspace = torch.empty(need, dtype=torch.uint8, device=pool.device)
-        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
-    err = d_error.data_ptr() if d_error is not None else None
-    st = _lib.lib().tq_paged_mixed(
-        dec_out.data_ptr(), dos, dec_q.data_ptr(), dqs, k_new.data_ptr(), ks, v_new.data_ptr(), vs,
-        dec_block_tables.data_ptr(), dbt, dec_block_tables.size(1), context_lens.data_ptr(), order, nd,
-        int(max_context_len), partition_tokens,
-        pre_out.data_ptr(), pos, pre_q.data_ptr(), pqs, pre_block_tables.data_ptr(), pbt, pre_block_tables.size(1),
-        cu_seqlens_q.data_ptr(), q_start.data_ptr(), npf, n_rows, int(max_query_len),
-        pool.data_ptr(), nb, n_layer, n_head, bs, d, layer, scale, ws_ptr, ws_bytes, err, _stream(pool.device),
-    )  # fmt: skip
-    _lib.check(st, "tq_paged_mixed")
+    if need and workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=pool.device)
+    if not need:
+        workspace = None
+    _op("paged_mixed", dec_out, dec_q, k_new, v_new, dec_block_tables, context_lens, int(max_context_len), pre_out,
+        pre_q, pre_block_tables, cu_seqlens_q, q_start, int(max_query_len), pool, layer, scale, partition_tokens,
+        workspace, d_error, seq_order)  # fmt: skip
 
 
 def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -294,11 +271,9 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.
         raise ValueError(f"out must be an int64 [{rows}] tensor on {logits.device}")
     elif rows > 1 and out.stride(0) != 1:
         raise ValueError("out must be contiguous")
-    stride = logits.stride(0) if rows > 1 else cols
     if cols > 1 and logits.stride(1) != 1:
         raise ValueError("logits rows must be contiguous")
-    st = _lib.lib().tq_argmax_rows(out.data_ptr(), logits.data_ptr(), rows, cols, stride, _stream(logits.device))
-    _lib.check(st, "tq_argmax_rows")
+    _op("argmax_rows", logits, out)
     return out
 
 
