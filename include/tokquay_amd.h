@@ -5,6 +5,7 @@
  * attention branch with hand-written HIP kernels:
  *
  *   tq_cache_write    scatter each new token's K/V rows into the block pool
+ *                     (tq_paged_gather: the reference view's gathered copy, for its callers)
  *   tq_paged_decode   one-query-per-sequence attention straight off the pool
  *   tq_paged_decode_write  the same, with the new token's cache write folded in
  *                     (tq_paged_decode_write_static: without a workspace argument)
@@ -216,6 +217,25 @@ tq_status tq_paged_decode_write_static(float* out, int64_t out_row_stride,
                                        int32_t num_seqs, int32_t max_context_len,
                                        float scale, int32_t partition_tokens,
                                        int32_t* d_error, void* stream);
+
+/*
+ * Gather: every sequence's K and V as the reference's batch view materialises them,
+ *
+ *   k_out[b][h][j * block_size + o][:] = pool[block_tables[b][j]][layer][0][h][o][:]
+ *   v_out[b][h][j * block_size + o][:] = pool[block_tables[b][j]][layer][1][h][o][:]
+ *
+ * for j < num_gathered_blocks (tables padded with any valid id, e.g. block 0, as the reference
+ * pads them), both outputs contiguous [num_seqs, num_heads, num_gathered_blocks * block_size,
+ * head_dim]. A bit-exact copy. An id outside the pool is reported (TQ_DEVERR_BLOCK_ID) and its
+ * keys come out as zeros. The attention entry points never need it; it serves callers of the
+ * reference's BatchedKV contract.
+ *
+ * Replaces PagedBatch.gather (tokquay/kv_cache.py:234-242).
+ */
+tq_status tq_paged_gather(float* k_out, float* v_out, const float* pool, int64_t num_blocks, int32_t num_layers,
+                          int32_t num_heads, int32_t block_size, int32_t head_dim, int32_t layer,
+                          const int32_t* block_tables, int64_t block_table_stride, int32_t num_gathered_blocks,
+                          int32_t num_seqs, int32_t* d_error, void* stream);
 
 /*
  * Paged prefill / chunked-prefill attention. Sequence b feeds

@@ -347,6 +347,68 @@ def test_mixed_entry_point_with_one_side_empty_and_bad_arguments():
         ops.paged_mixed(o3d, dq, dk, dv, dtab, dctx, maxc, o3p, pq, ptab, cu[:-1], qst, maxq, p3, sc.layer)
 
 
+# ------------------------------------------------------------------------------ the reference view's gather
+@pytest.mark.parametrize("block_size", [1, 8, 16, 32])
+def test_gather_equals_the_reference_gather(block_size):
+    """PagedBatch.gather (the HIP gather kernel) == the reference's PagedBatch.gather bit for bit on a
+    garbage pool with shuffled tables, after the step's write; padded table entries read block 0 as
+    the reference's do (tokquay/kv_cache.py:195-200, :234-242)."""
+    from oracle.paged_ref import RefPagedBatch
+    from tokquay_amd.kv_cache import PagedBatch
+
+    starts = [0, 37, 100, 5, 250, 0]
+    lens = [23, 1, 1, 40, 3, 1]
+    sc = Scenario(starts, lens, block_size=block_size, n_layer=2, layer=1, seed=30 + block_size)
+    ref_pool = sc.pool.clone()
+    ref = RefPagedBatch(ref_pool, block_size, sc.tables, sc.starts, sc.new_lens)
+    ref.write(sc.layer, sc.k, sc.v)
+    rk, rv = ref.gather(sc.layer)
+
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    pool = sc.pool.cuda()
+    batch = PagedBatch(pool, block_size, sc.tables, sc.starts, sc.new_lens, error_word=err)
+    batch.write(sc.layer, sc.k.cuda(), sc.v.cuda())
+    k, v = batch.gather(sc.layer)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    assert k.shape == rk.shape and v.shape == rv.shape
+    assert torch.equal(k.cpu(), rk) and torch.equal(v.cpu(), rv)
+    assert torch.equal(pool.cpu(), ref_pool)
+
+
+def test_the_reference_attention_branch_runs_on_the_product_batch_view():
+    """The reference's paged branch of Attention.forward unchanged - write, gather, masked softmax
+    (tokquay/model.py:73-78, :94-96) - on tokquay_amd.PagedBatch (write and gather on the HIP kernels,
+    the softmax in torch on the CPU) equals PagedBatch.attend at fp32 tolerance."""
+    from oracle.paged_ref import ref_attention
+    from tokquay_amd.kv_cache import PagedBatch
+
+    starts, lens = mixed_case("tiny")
+    starts, lens = starts + [0, 60], lens + [17, 1]
+    sc = Scenario(starts, lens, block_size=16, seed=41)
+    pool = sc.pool.cuda()
+    batch = PagedBatch(pool, 16, sc.tables, sc.starts, sc.new_lens)
+    batch.write(sc.layer, sc.k.cuda(), sc.v.cuda())
+    k, v = batch.gather(sc.layer)
+    got = ref_attention(sc.q, k.cpu(), v.cpu(), batch.mask.cpu())  # [B, H, T, d]
+    _, out_gpu, b2 = sc.run_product()
+    want = sc.packed_reference(got, b2.token_index)
+    torch.testing.assert_close(out_gpu, want, rtol=RTOL, atol=ATOL)
+
+
+def test_gather_reports_a_bad_block_id_and_zeroes_its_keys():
+    from tokquay_amd import _lib, ops
+
+    pool = torch.randn(4, 1, 2, 12, 16, 64, device="cuda")
+    tables = torch.tensor([[0, 3], [2, 9]], dtype=torch.int32, device="cuda")  # 9 is outside the pool
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    k, v = ops.paged_gather(pool, 0, tables, err)
+    torch.cuda.synchronize()
+    assert int(err.item()) & _lib.DEVERR_BLOCK_ID
+    assert torch.equal(k[0, :, 16:], pool[3, 0, 0]) and torch.equal(v[1, :, :16], pool[2, 0, 1])
+    assert not k[1, :, 16:].any() and not v[1, :, 16:].any()
+
+
 # ------------------------------------------------------------------------------ contract edges
 def test_write_contract_padded_layout_is_bit_exact_and_padding_never_writes():
     """BatchedKV.write with the reference's [B, H, T, d] layout: padded positions write nothing and

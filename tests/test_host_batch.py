@@ -86,9 +86,10 @@ def test_validation_matches_reference_errors():
         PagedBatch(pool, 4, [[0]], [0], [9])  # one block for 9 tokens (tests/test_phase3_paged.py:185-190)
 
 
-def test_gather_is_not_materialised():
-    pool = torch.zeros(8, 1, 2, 1, 4, 4)
-    with pytest.raises(NotImplementedError):
+def test_gather_refuses_a_cpu_pool():
+    """gather runs on the HIP gather kernel only (no CPU fallback); its parity is a GPU test."""
+    pool = torch.zeros(8, 1, 2, 1, 4, 64)
+    with pytest.raises(ValueError):
         PagedBatch(pool, 4, [[0, 1]], [0], [5]).gather(0)
 
 

@@ -21,6 +21,7 @@ def test_every_operator_is_registered_with_its_mutations():
     assert "Tensor(a!) out" in schemas["paged_prefill"] and "Tensor pool" in schemas["paged_prefill"]
     assert "Tensor(a!) dec_out" in schemas["paged_mixed"] and "Tensor(b!) pre_out" in schemas["paged_mixed"]
     assert "Tensor(c!) pool" in schemas["paged_mixed"]
+    assert "Tensor(a!) k_out" in schemas["paged_gather"] and "Tensor(b!) v_out" in schemas["paged_gather"]
     assert "Tensor(a!) out" in schemas["argmax_rows"]
     for s in schemas.values():
         assert s.endswith("-> ()")

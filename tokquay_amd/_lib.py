@@ -86,6 +86,15 @@ SIGNATURES: dict[str, tuple] = {
             c_i32p, ctypes.c_void_p,  # d_error, stream
         ],
     ),
+    "tq_paged_gather": (
+        ctypes.c_int,
+        [
+            c_f32p, c_f32p, c_f32p, ctypes.c_int64, ctypes.c_int32,  # k_out, v_out, pool, num_blocks, num_layers
+            ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,  # num_heads, block_size, head_dim, layer
+            c_i32p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,  # block_tables, stride, gathered blocks, num_seqs
+            c_i32p, ctypes.c_void_p,  # d_error, stream
+        ],
+    ),
     "tq_paged_decode_workspace_size": (
         ctypes.c_size_t,
         [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32],

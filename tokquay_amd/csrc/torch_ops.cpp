@@ -126,6 +126,16 @@ void paged_mixed(at::Tensor dec_out, const at::Tensor& dec_q, const at::Tensor& 
         "tq_paged_mixed");
 }
 
+void paged_gather(at::Tensor k_out, at::Tensor v_out, const at::Tensor& pool, int64_t layer,
+                  const at::Tensor& block_tables, const c10::optional<at::Tensor>& d_error) {
+  const Pool p = pool_of(pool);
+  check(tq_paged_gather(k_out.data_ptr<float>(), v_out.data_ptr<float>(), pool.data_ptr<float>(), p.blocks, p.layers,
+                        p.heads, p.block_size, p.head_dim, (int32_t)layer, block_tables.data_ptr<int32_t>(),
+                        table_stride(block_tables), (int32_t)block_tables.size(1), (int32_t)block_tables.size(0),
+                        ptr<int32_t>(d_error), stream_of(pool)),
+        "tq_paged_gather");
+}
+
 void argmax_rows(const at::Tensor& logits, at::Tensor out) {
   const int64_t stride = logits.size(0) > 1 ? logits.stride(0) : logits.size(1);
   check(tq_argmax_rows(out.data_ptr<int64_t>(), logits.data_ptr<float>(), logits.size(0), logits.size(1), stride,
@@ -149,6 +159,8 @@ TORCH_LIBRARY(tokquay_amd, m) {
         "Tensor context_lens, int max_context_len, Tensor(b!) pre_out, Tensor pre_q, Tensor pre_block_tables, "
         "Tensor cu_seqlens_q, Tensor q_start, int max_query_len, Tensor(c!) pool, int layer, float scale, "
         "int partition_tokens, Tensor? workspace, Tensor(d!)? d_error, Tensor? seq_order) -> ()");
+  m.def("paged_gather(Tensor(a!) k_out, Tensor(b!) v_out, Tensor pool, int layer, Tensor block_tables, "
+        "Tensor(c!)? d_error) -> ()");
   m.def("argmax_rows(Tensor logits, Tensor(a!) out) -> ()");
 }
 
@@ -158,5 +170,6 @@ TORCH_LIBRARY_IMPL(tokquay_amd, CUDA, m) {
   m.impl("paged_decode_write", &paged_decode_write);
   m.impl("paged_prefill", &paged_prefill);
   m.impl("paged_mixed", &paged_mixed);
+  m.impl("paged_gather", &paged_gather);
   m.impl("argmax_rows", &argmax_rows);
 }

@@ -218,6 +218,7 @@ class PagedBatch(BatchedKV):
         self.num_blocks_gathered = plan["max_blocks"]
         self.max_ctx = plan["max_ctx"]
         self.start, self.new_lens = start, new_lens
+        self._tables = tables  # the callers' lists, for the reference view's gather
         self.error_word = error_word
         self.partition_tokens = partition_tokens
         device = pool.device
@@ -345,9 +346,17 @@ class PagedBatch(BatchedKV):
         ops.cache_write(self.pool, layer, rows[0], rows[1], self.padded_slot_mapping(), self.error_word)
 
     def gather(self, layer: int) -> tuple[torch.Tensor, torch.Tensor]:
-        raise NotImplementedError(
-            "the gfx950 batch view never materialises gathered K/V: attend(layer, qkv) reads the pool in place"
-        )
+        """Each sequence's K and V as contiguous ``[B, H, nb * block_size, d]`` (tokquay/kv_cache.py:
+        234-242): tables padded to ``nb`` entries with block 0, copied by the HIP gather kernel bit
+        for bit. The attention path never needs this copy (``attend`` reads the pool in place); it
+        serves callers of the reference's ``BatchedKV`` contract."""
+        from tokquay_amd import ops
+
+        if "gather_tables" not in self._lazy:
+            nb = self.num_blocks_gathered
+            padded = [list(t[:nb]) + [0] * (nb - len(t[:nb])) for t in self._tables]
+            self._lazy["gather_tables"] = torch.tensor(padded, dtype=torch.int32).to(self.device)
+        return ops.paged_gather(self.pool, layer, self._lazy["gather_tables"], self.error_word)
 
     # ---- the HIP path ----------------------------------------------------------------
     def attend(self, layer: int, qkv: torch.Tensor) -> torch.Tensor:

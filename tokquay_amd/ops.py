@@ -257,6 +257,22 @@ def paged_mixed(
         workspace, d_error, seq_order)  # fmt: skip
 
 
+def paged_gather(pool: torch.Tensor, layer: int, block_tables: torch.Tensor,
+                 d_error: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Every sequence's K and V ``[B, H, nb * block_size, d]`` gathered from ``pool[:, layer]`` in
+    table order (``block_tables`` int32 ``[B, nb]``, padded with any valid id): the copy the
+    reference's ``PagedBatch.gather`` materialises (tokquay/kv_cache.py:234-242), bit for bit."""
+    nb, n_layer, n_head, bs, d = _pool_dims(pool)
+    if not 0 <= layer < n_layer:
+        raise ValueError(f"layer {layer} out of range [0, {n_layer})")
+    B = block_tables.size(0)
+    _tables(block_tables, "block_tables", B, pool.device)
+    k = torch.empty(B, n_head, block_tables.size(1) * bs, d, dtype=torch.float32, device=pool.device)
+    v = torch.empty_like(k)
+    _op("paged_gather", k, v, pool, layer, block_tables, d_error)
+    return k, v
+
+
 def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """Greedy ids ``[R]`` (int64) of float32 logits ``[R, V]``: the reference's ``logits.argmax(-1)``
     (tokquay/engine.py:190) - the lowest index of each row's maximum, NaN above every number."""

@@ -1,6 +1,6 @@
 """``torch.ops.tokquay_amd.*``: the paged-attention entry points as torch operators.
 
-``csrc/torch_ops.cpp`` (built into ``_torch_ops.so`` next to ``libtokquay_amd.so``) registers six
+``csrc/torch_ops.cpp`` (built into ``_torch_ops.so`` next to ``libtokquay_amd.so``) registers seven
 out-variant operators with torch's dispatcher; each is a thin call into the C ABI on the current
 HIP stream. This module loads that library and registers the operators' fake (shape-only)
 implementations, so programs that record torch calls (``make_fx``, FX graphs on fake tensors)
@@ -15,6 +15,8 @@ see the kernels as single operators:
 * ``paged_mixed(dec_out!, dec_q, k_new, v_new, dec_block_tables, context_lens, max_context_len,
   pre_out!, pre_q, pre_block_tables, cu_seqlens_q, q_start, max_query_len, pool!, layer, scale,
   partition_tokens, workspace?, d_error!?, seq_order?)``
+* ``paged_gather(k_out!, v_out!, pool, layer, block_tables, d_error!?)`` (the reference view's
+  gathered copy)
 * ``argmax_rows(logits, out!)``
 
 (``!``: written in place.) ``tokquay_amd.ops`` checks the tensors with the reference's messages
@@ -29,7 +31,8 @@ import torch
 
 from tokquay_amd.build import TORCH_OPS_PATH
 
-OPS = ("cache_write", "paged_decode", "paged_decode_write", "paged_prefill", "paged_mixed", "argmax_rows")
+OPS = ("cache_write", "paged_decode", "paged_decode_write", "paged_prefill", "paged_mixed", "paged_gather",
+       "argmax_rows")
 
 _loaded = False
 
