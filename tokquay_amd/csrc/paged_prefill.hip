@@ -237,8 +237,25 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
   // B operand of the QK product: Q[query j][16g + s], s = 0..15, pre-scaled by
   // scale * log2(e) so the scores come out in log2 units for v_exp_f32.
   const float qscale = a.scale * kLog2e;
+  // The pipelined key split (block size 16, 2 or 4 waves) reads the tile's Q once per workgroup:
+  // wave w loads float4 columns w, w + KS, ... of every lane's 16 dims here and the waves swap
+  // them through LDS after issuing their first key tile's loads. At a launch's start every wave
+  // otherwise asks for all of Q and two key tiles at once; sharing Q cuts that burst by 12 KB per
+  // 4-wave workgroup (config 5's chunk launches 11.7 / 20.0 / 27.1 -> 10.9 / 19.0 / 26.0 us).
+  constexpr bool kSharedQ = BS_CT == kTile && KS > 1 && KS <= 4;
+  constexpr int kQShare = (4 + KS - 1) / KS;
+  float4 qshare[kQShare];
   float qreg[16];
-  if (q_ok) {
+  if constexpr (kSharedQ) {
+#pragma unroll
+    for (int i = 0; i < kQShare; ++i) {
+      const int v = wave + KS * i;  // wave-uniform
+      qshare[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (q_ok && v < 4)
+        qshare[i] = *reinterpret_cast<const float4*>(a.q + (int64_t)(row0 + qi) * a.q_stride + h * kHeadDim +
+                                                     16 * g + 4 * v);
+    }
+  } else if (q_ok) {
     const float* qp = a.q + (int64_t)(row0 + qi) * a.q_stride + h * kHeadDim + 16 * g;
 #pragma unroll
     for (int v4 = 0; v4 < 4; ++v4) {
@@ -369,10 +386,30 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
     };
     const int step = KS * kTile;
     int kt = wave * kTile;
-    if (kt < kend) {
-      float ka[16], kb[16];
-      float4 va[4], vb[4];
-      int32_t ba = fetch(kt, ka, va), bb;
+    const bool any = kt < kend;  // wave-uniform
+    float ka[16], kb[16];
+    float4 va[4], vb[4];
+    int32_t ba = -1, bb;
+    if (any) ba = fetch(kt, ka, va);
+    if constexpr (kSharedQ) {
+      // Every wave, also one with no key tile, stages its Q columns; then all read the tile.
+      __shared__ float s_q[kTile][kHeadDim];
+#pragma unroll
+      for (int i = 0; i < kQShare; ++i) {
+        const int v = wave + KS * i;
+        if (v < 4) *reinterpret_cast<float4*>(&s_q[j][16 * g + 4 * v]) = qshare[i];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int v4 = 0; v4 < 4; ++v4) {
+        const float4 x = *reinterpret_cast<const float4*>(&s_q[j][16 * g + 4 * v4]);
+        qreg[4 * v4 + 0] = x.x * qscale;
+        qreg[4 * v4 + 1] = x.y * qscale;
+        qreg[4 * v4 + 2] = x.z * qscale;
+        qreg[4 * v4 + 3] = x.w * qscale;
+      }
+    }
+    if (any) {
       while (true) {
         // Always issue the next loads (the last tile re-reads itself), so the wait
         // counts before each tile's math are the same on every path.
