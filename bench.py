@@ -84,11 +84,19 @@ def prefill_flops(starts: list[int], lens: list[int], n_head: int = N_HEAD, d: i
     return sum(4 * n_head * d * (n * s + n * (n + 1) // 2) for s, n in zip(starts, lens))
 
 
+# A spin of this many shader clock cycles (~0.2 ms on MI355X) per launch to be queued: the
+# op-alone measurement enqueues its launches behind one long spin so that they run back to back
+# (a launch that finds the GPU idle starts its 8 XCDs up to ~4 us apart, measured with per-wave
+# timestamps, which inflates a 15 us launch by a tenth).
+QUEUE_AHEAD_CYCLES = 500_000
+
+
 class LaunchTimer:
     """Times attention launches per kind - "decode", "prefill", or "mixed" (both kinds of row in one
     tq_paged_mixed launch) - with HIP events that the launch itself records at the start and end of
     its kernels (tq_set_timing_events), and adds up each kind's algorithmic decode bytes and prefill
-    flops."""
+    flops. Its bookkeeping is O(rows) per launch, so an eager step's host work stays short and the
+    launches run close together as in the graph-replayed steps."""
 
     def __init__(self, *kinds: str):
         import torch
@@ -108,12 +116,12 @@ class LaunchTimer:
         stop.record()
         self.lib.tq_set_timing_events(start.cuda_event, stop.cuda_event)
         self.pairs[kind].append((start, stop))
-        dec = [b for b in range(batch.B) if batch.new_lens[b] == 1]
-        pre = [b for b in range(batch.B) if batch.new_lens[b] != 1]
+        starts, lens = batch.start, batch.new_lens  # lists; batch.context_lens builds a new one per access
         if kind in ("decode", "mixed"):
-            self.bytes[kind] += decode_bytes([batch.context_lens[b] for b in dec])
+            self.bytes[kind] += decode_bytes([s + 1 for s, n in zip(starts, lens) if n == 1])
         if kind in ("prefill", "mixed"):
-            self.flops[kind] += prefill_flops([batch.start[b] for b in pre], [batch.new_lens[b] for b in pre])
+            pre = [(s, n) for s, n in zip(starts, lens) if n != 1]
+            self.flops[kind] += prefill_flops([s for s, _ in pre], [n for _, n in pre])
 
     def launches(self, kind: str) -> int:
         return len(self.pairs[kind])
@@ -191,10 +199,13 @@ def decode_op_alone(seed: int = 2) -> dict:
     """The decode kernel alone on the op-alone shape: 64 sequences, 12 heads, head_dim 64,
     contexts U[16, 512] (redrawn with seeds 0, 1, ... until they fit the 1,024-block pool), block
     size 16, block tables a seeded random permutation, Q and the pool ~ N(0, 1), one query per
-    sequence; a 1-layer pool. Median of 200 back-to-back launches timed with HIP events."""
+    sequence; a 1-layer pool. Median of 200 launches timed with HIP events the launch records around
+    its kernels, enqueued behind one long spin kernel so that they run back to back as in a model
+    step; the median of 200 launches paced by the host (each one finding the GPU idle, its events
+    recorded around the call) is reported beside it."""
     import torch
 
-    from tokquay_amd import ops
+    from tokquay_amd import _lib, ops
 
     draw = 0
     while True:
@@ -220,21 +231,36 @@ def decode_op_alone(seed: int = 2) -> dict:
     call = lambda: ops.paged_decode(out, q, pool, 0, tables, lens, max(ctx), seq_order=order)  # noqa: E731
     for _ in range(10):
         call()
-    times = []
+    lib = _lib.lib()
+    torch.cuda.synchronize()
+    torch.cuda._sleep(200 * QUEUE_AHEAD_CYCLES)  # ~40 ms: the host enqueues all 200 launches behind it
+    queued = []
+    for _ in range(200):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        b.record()
+        lib.tq_set_timing_events(a.cuda_event, b.cuda_event)  # re-recorded at the kernel's start and end
+        call()
+        queued.append((a, b))
+    torch.cuda.synchronize()
+    paced = []
     for _ in range(200):
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
         call()
         b.record()
-        times.append((a, b))
+        paced.append((a, b))
     torch.cuda.synchronize()
-    us = statistics.median(a.elapsed_time(b) for a, b in times) * 1e3
+    us = statistics.median(a.elapsed_time(b) for a, b in queued) * 1e3
+    us_paced = statistics.median(a.elapsed_time(b) for a, b in paced) * 1e3
     nbytes = decode_bytes(ctx, write=False)
     return {"workload": f"decode op alone: 64 sequences, ctx U[16,512] (draw seed {draw}, {sum(ctx)} positions), "
-                        "12 heads x 64, block 16, 1,024-block pool (1 layer), random block permutation",
+                        "12 heads x 64, block 16, 1,024-block pool (1 layer), random block permutation; "
+                        "launches queued back to back",
             "draw_seed": draw,
             "kernel": "tq_paged_decode", "us_per_call": round(us, 2), "bytes_per_call": nbytes,
-            "achieved_GBs": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}  # fmt: skip
+            "achieved_GBs": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+            "us_per_call_host_paced": round(us_paced, 2)}  # fmt: skip
 
 
 def mixed_chunked_step(seed: int = 5) -> tuple[dict, dict]:

@@ -451,29 +451,3 @@ class PagedBatch(BatchedKV):
                 "tq_paged_prefill",
             )  # fmt: skip
         return out
-
-        # Per-kernel launches, with the hook armed before each attention kernel.
-        if Bd:
-            PagedBatch.launch_hook(self, "decode")
-            _lib.check(
-                L.tq_paged_decode_write(op, C, qp, row3, qp + 4 * C, row3, qp + 8 * C, row3, pp, nb, n_layer,
-                                        n_head, bs, d, layer, self._ptr32(0), self._nbd, self._nbd, self._ptr32(1),
-                                        self._ptr32(5), Bd, self.decode_max_ctx, scale, self.partition_tokens, ws,
-                                        self._ws_bytes, err, stream),
-                "tq_paged_decode_write",
-            )  # fmt: skip
-        if Bp:
-            off = Bd * row3 * 4  # bytes to the first prefill row of qkv
-            _lib.check(
-                L.tq_cache_write(pp, nb, n_layer, n_head, bs, d, layer, qp + off + 4 * C, row3, qp + off + 8 * C,
-                                 row3, slots + 8 * Bd, N - Bd, err, stream),
-                "tq_cache_write",
-            )  # fmt: skip
-            PagedBatch.launch_hook(self, "prefill")
-            _lib.check(
-                L.tq_paged_prefill(op + 4 * Bd * C, C, qp + off, row3, pp, nb, n_layer, n_head, bs, d, layer,
-                                   self._ptr32(2), self._nbp, self._nbp, self._ptr32(3), self._ptr32(4), Bp, N - Bd,
-                                   self.prefill_max_q, scale, err, stream),
-                "tq_paged_prefill",
-            )  # fmt: skip
-        return out
