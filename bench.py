@@ -875,7 +875,8 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "tq_paged_decode_write (decode_partition_kernel; decode_merge_kernel when a sequence spans several partitions)",
+            "kernel": "tq_paged_decode_write (decode_split_kernel: W waves per (sequence, head) splitting its "
+            "context, merged in LDS; W = 8 at contexts of 897-1024)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
