@@ -162,11 +162,30 @@ def test_decode_config4_scale():
 
 @pytest.mark.parametrize("block_size", [8, 32])
 def test_decode_full_grid_other_block_sizes(block_size):
-    """256 sequences at contexts U[1, 1024]: the automatic choice is the one-wave-per-sequence grid
-    with the snaked dispatch order, here on the block-size-32 instance and the generic one."""
+    """256 sequences at contexts U[1, 1024]: the automatic choice splits each (sequence, head) over
+    8 waves, here on the block-size-32 instance and the generic one."""
     rng = random.Random(block_size + 100)
     ctx = [rng.randint(1, 1024) for _ in range(256)]
     sc = Scenario([c - 1 for c in ctx], [1] * 256, block_size=block_size, seed=block_size + 100)
+    check(sc, brute=False)
+
+
+@pytest.mark.parametrize("max_ctx", [128, 129, 256, 257, 512, 513, 1024])
+def test_decode_automatic_split_width_boundaries(max_ctx):
+    """The automatic grid at 256 sequences: one wave per (sequence, head) up to 128 positions, then
+    2, 4 or 8 waves per pair (about 128 positions per wave at the longest context), each width on
+    both sides of its boundary, against the reference path."""
+    rng = random.Random(max_ctx)
+    ctx = [rng.randint(max(1, max_ctx // 2), max_ctx) for _ in range(255)] + [max_ctx]
+    sc = Scenario([c - 1 for c in ctx], [1] * 256, block_size=16, seed=max_ctx)
+    check(sc, brute=False)
+
+
+@pytest.mark.parametrize("ctx", [[9000, 5000, 300], [16384, 1, 700], [17000, 40]])
+def test_decode_long_contexts_split_or_partition_grid(ctx):
+    """Small batches at long contexts: 16 waves per (sequence, head) while the longest context fits
+    16 x 1024 positions, the partition grid with its merge launch beyond."""
+    sc = Scenario([c - 1 for c in ctx], [1] * len(ctx), block_size=16, seed=len(ctx) + ctx[0])
     check(sc, brute=False)
 
 
