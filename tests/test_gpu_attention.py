@@ -523,13 +523,26 @@ def test_launch_recorded_timing_events():
 def test_prefill_key_split_widths(block_size, num_seqs):
     """The prefill launch splits each query tile's keys over 1, 2, 4 or 8 waves depending on how many
     tiles there are (4608 / 1536 / 768 / 192 query tiles -> 1 / 2 / 4 / 8 waves), for the
-    block-size-16 path (one block per key tile; software-pipelined up to 4 waves) and the generic
-    one; every width must match the reference, with ragged lengths and chunk starts."""
+    block-size-16 path (one block per key tile; software-pipelined up to 4 waves; the one-wave
+    launch takes two query tiles per wave) and the generic one; every width must match the
+    reference, with ragged lengths and chunk starts."""
     rng = random.Random(num_seqs)
     lens = [256] + [rng.randint(100, 256) for _ in range(num_seqs - 1)]
     starts = [rng.choice([0, 0, 100, 300]) for _ in range(num_seqs)]
     sc = Scenario(starts, lens, block_size=block_size, seed=90 + num_seqs)
     check(sc, brute=num_seqs <= 6)
+
+
+def test_prefill_two_query_tiles_per_wave_edges():
+    """A launch of more than 1536 query tiles and at least 8192 row tiles at block size 16 gives each
+    wave two consecutive query tiles: lengths that leave the second tile partly or wholly empty,
+    starts inside a block."""
+    rng = random.Random(77)
+    base = [2, 15, 16, 17, 31, 32, 33, 47, 48, 49, 64, 65]
+    lens = [base[i % len(base)] for i in range(320)]  # 11,087 rows: 12 x 693 = 8,316 row tiles
+    starts = [rng.choice([0, 5, 16, 100]) for _ in lens]
+    sc = Scenario(starts, lens, block_size=16, seed=77)
+    check(sc, brute=False)
 
 
 @pytest.mark.parametrize("block_size", [8, 16])

@@ -204,10 +204,12 @@ __device__ __forceinline__ void load_kv_block_tile(const PrefillArgs& a, const f
   }
 }
 
-// The work of prefill workgroup `dispatch` (its KS waves): one query tile of one head of one
-// sequence, or nothing for a padding workgroup.
-template <int BS_CT, int KS>
+// The work of prefill workgroup `dispatch` (its KS waves): QH consecutive query tiles of one head
+// of one sequence, or nothing for a padding workgroup. QH = 2 (one wave per workgroup only) feeds
+// each key tile's loads to twice the MFMAs and gives the wave two independent softmax chains.
+template <int BS_CT, int KS, int QH = 1>
 __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int dispatch) {
+  static_assert(QH == 1 || KS == 1, "two query tiles per wave only without a key split");
   const int lane = threadIdx.x & (kWave - 1);
   // Wave-uniform by construction; readfirstlane lets the compiler keep the key-tile loop
   // (counter, bounds, branches) in scalar registers.
@@ -218,7 +220,7 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
 
   const int row0 = a.cu_q[b];
   const int nq = a.cu_q[b + 1] - row0;
-  const int qi0 = qt * kTile;
+  const int qi0 = qt * kTile * QH;
   if (qi0 >= nq) return;
   const int start = a.q_start[b];
   if (row0 < 0 || row0 + nq > a.num_q_rows || start < 0 ||
@@ -229,10 +231,18 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
 
   const int j = lane & 15;  // query column of this lane (and dim group i of the PV A operand)
   const int g = lane >> 4;  // lane group: dims 16g..16g+15 in QK, keys 4g..4g+3 in PV
-  const int qi = qi0 + j;
-  const bool q_ok = qi < nq;
-  const int qpos = start + (q_ok ? qi : nq - 1);  // padded lanes mirror the last real query
-  const int qpos_lo = start + qi0;                 // the tile's first query position
+  // Query tile u of the wave holds queries qi0 + 16 u + j.
+  bool q_ok[QH];
+  int qpos[QH];     // padded lanes mirror the last real query
+  int qpos_lo[QH];  // the tile's first query position
+#pragma unroll
+  for (int u = 0; u < QH; ++u) {
+    const int qu = qi0 + 16 * u + j;
+    q_ok[u] = qu < nq;
+    qpos[u] = start + (q_ok[u] ? qu : nq - 1);
+    qpos_lo[u] = start + qi0 + 16 * u;
+  }
+  const int qi = qi0 + j;  // the lane's query in tile 0
 
   // B operand of the QK product: Q[query j][16g + s], s = 0..15, pre-scaled by
   // scale * log2(e) so the scores come out in log2 units for v_exp_f32.
@@ -245,90 +255,111 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
   constexpr bool kSharedQ = BS_CT == kTile && KS > 1 && KS <= 4;
   constexpr int kQShare = (4 + KS - 1) / KS;
   float4 qshare[kQShare];
-  float qreg[16];
+  float qreg[QH][16];
   if constexpr (kSharedQ) {
 #pragma unroll
     for (int i = 0; i < kQShare; ++i) {
       const int v = wave + KS * i;  // wave-uniform
       qshare[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (q_ok && v < 4)
+      if (q_ok[0] && v < 4)
         qshare[i] = *reinterpret_cast<const float4*>(a.q + (int64_t)(row0 + qi) * a.q_stride + h * kHeadDim +
                                                      16 * g + 4 * v);
     }
-  } else if (q_ok) {
-    const float* qp = a.q + (int64_t)(row0 + qi) * a.q_stride + h * kHeadDim + 16 * g;
-#pragma unroll
-    for (int v4 = 0; v4 < 4; ++v4) {
-      const float4 x = *reinterpret_cast<const float4*>(qp + 4 * v4);
-      qreg[4 * v4 + 0] = x.x * qscale;
-      qreg[4 * v4 + 1] = x.y * qscale;
-      qreg[4 * v4 + 2] = x.z * qscale;
-      qreg[4 * v4 + 3] = x.w * qscale;
-    }
   } else {
 #pragma unroll
-    for (int s = 0; s < 16; ++s) qreg[s] = 0.f;
+    for (int u = 0; u < QH; ++u) {
+      if (q_ok[u]) {
+        const float* qp = a.q + (int64_t)(row0 + qi + 16 * u) * a.q_stride + h * kHeadDim + 16 * g;
+#pragma unroll
+        for (int v4 = 0; v4 < 4; ++v4) {
+          const float4 x = *reinterpret_cast<const float4*>(qp + 4 * v4);
+          qreg[u][4 * v4 + 0] = x.x * qscale;
+          qreg[u][4 * v4 + 1] = x.y * qscale;
+          qreg[u][4 * v4 + 2] = x.z * qscale;
+          qreg[u][4 * v4 + 3] = x.w * qscale;
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < 16; ++s) qreg[u][s] = 0.f;
+      }
+    }
   }
 
   const int32_t* bt = a.block_tables + (int64_t)b * a.bt_stride;
   const float* head_base = a.pool_layer + (int64_t)h * a.head_stride;
-  const int kend = start + min(qi0 + kTile, nq);  // keys this tile can see: [0, kend)
+  const int kend = start + min(qi0 + kTile * QH, nq);  // keys the wave's tiles can see: [0, kend)
 
-  floatx4 o[4];
+  floatx4 o[QH][4];
+  float m[QH], l[QH];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) o[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY;
-  float l = 0.f;
+  for (int u = 0; u < QH; ++u) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) o[u][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    m[u] = -INFINITY;
+    l[u] = 0.f;
+  }
 
   // Wave w of the workgroup visits key tiles w, w + KS, w + 2 KS, ...: the QK A
   // operand K[kt + j][16g + s] and the PV A operand rows V[kt + 4g + s][4j .. 4j+3].
-  // One key tile's math: S^T = K Q^T, the online-softmax update, O^T += V^T P^T.
+  // One key tile's math for each query tile: S^T = K Q^T, the online-softmax update,
+  // O^T += V^T P^T.
   auto consume = [&](int kt, const float (&kreg)[16], const float4 (&vreg)[4]) {
-      // Two independent MFMA chains (even / odd dim groups) halve the dependent latency.
-      floatx4 st0 = {0.f, 0.f, 0.f, 0.f}, st1 = {0.f, 0.f, 0.f, 0.f};
+      // Two independent MFMA chains (even / odd dim groups) per query tile halve the dependent
+      // latency.
+      floatx4 st0[QH], st1[QH];
+  #pragma unroll
+      for (int u = 0; u < QH; ++u) st0[u] = st1[u] = floatx4{0.f, 0.f, 0.f, 0.f};
   #pragma unroll
       for (int s = 0; s < 16; s += 2) {
-        st0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kreg[s], qreg[s], st0, 0, 0, 0);
-        st1 = __builtin_amdgcn_mfma_f32_16x16x4f32(kreg[s + 1], qreg[s + 1], st1, 0, 0, 0);
+  #pragma unroll
+        for (int u = 0; u < QH; ++u) {
+          st0[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(kreg[s], qreg[u][s], st0[u], 0, 0, 0);
+          st1[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(kreg[s + 1], qreg[u][s + 1], st1[u], 0, 0, 0);
+        }
       }
-      const floatx4 st = st0 + st1;  // st[r] = S^T[key kt + 4g + r][query j], log2 units
-
-      float sm[4];
-      if (kt + kTile - 1 > qpos_lo) {  // uniform: the tile crosses the causal diagonal
+      float p[QH][4];
   #pragma unroll
-        for (int r = 0; r < 4; ++r) sm[r] = kt + 4 * g + r <= qpos ? st[r] : -INFINITY;
-      } else {
+      for (int u = 0; u < QH; ++u) {
+        const floatx4 st = st0[u] + st1[u];  // st[r] = S^T[key kt + 4g + r][query j], log2 units
+        float sm[4];
+        if (kt + kTile - 1 > qpos_lo[u]) {  // uniform: the key tile crosses this query tile's diagonal
   #pragma unroll
-        for (int r = 0; r < 4; ++r) sm[r] = st[r];
+          for (int r = 0; r < 4; ++r) sm[r] = kt + 4 * g + r <= qpos[u] ? st[r] : -INFINITY;
+        } else {
+  #pragma unroll
+          for (int r = 0; r < 4; ++r) sm[r] = st[r];
+        }
+        float tmax = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
+        tmax = max_over_lane_groups(tmax);
+        // Lazy rescale: the reference maximum m moves only when a score exceeds it by
+        // more than kSlack (log2 units), so p <= 2^kSlack and the accumulators are
+        // rescaled on few tiles. The test is wave-uniform through the ballot.
+        const bool grow = tmax > m[u] + kSlack;  // false while the query has seen no key
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+          const float mn = grow ? tmax : m[u];
+          const float corr = grow ? __builtin_amdgcn_exp2f(m[u] - mn) : 1.f;  // m = -inf: 0
+          l[u] *= corr;
+  #pragma unroll
+          for (int t = 0; t < 4; ++t) o[u][t] *= corr;
+          m[u] = mn;
+        }
+        // A query with no visible key so far (m = -inf) has only -inf scores here:
+        // any finite reference gives p = 0 and keeps its state exactly zero.
+        const float mref = m[u] == -INFINITY ? 0.f : m[u];
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) p[u][r] = __builtin_amdgcn_exp2f(sm[r] - mref);
+        l[u] += (p[u][0] + p[u][1]) + (p[u][2] + p[u][3]);
       }
-      float tmax = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
-      tmax = max_over_lane_groups(tmax);
-      // Lazy rescale: the reference maximum m moves only when a score exceeds it by
-      // more than kSlack (log2 units), so p <= 2^kSlack and the accumulators are
-      // rescaled on few tiles. The test is wave-uniform through the ballot.
-      const bool grow = tmax > m + kSlack;  // false while the query has seen no key
-      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-        const float mn = grow ? tmax : m;
-        const float corr = grow ? __builtin_amdgcn_exp2f(m - mn) : 1.f;  // m = -inf: 0
-        l *= corr;
-  #pragma unroll
-        for (int t = 0; t < 4; ++t) o[t] *= corr;
-        m = mn;
-      }
-      // A query with no visible key so far (m = -inf) has only -inf scores here:
-      // any finite reference gives p = 0 and keeps its state exactly zero.
-      const float mref = m == -INFINITY ? 0.f : m;
-      float p[4];
-  #pragma unroll
-      for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(sm[r] - mref);
-      l += (p[0] + p[1]) + (p[2] + p[3]);
 
   #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        o[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(vreg[s].x, p[s], o[0], 0, 0, 0);
-        o[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(vreg[s].y, p[s], o[1], 0, 0, 0);
-        o[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(vreg[s].z, p[s], o[2], 0, 0, 0);
-        o[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vreg[s].w, p[s], o[3], 0, 0, 0);
+  #pragma unroll
+        for (int u = 0; u < QH; ++u) {
+          o[u][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(vreg[s].x, p[u][s], o[u][0], 0, 0, 0);
+          o[u][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(vreg[s].y, p[u][s], o[u][1], 0, 0, 0);
+          o[u][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(vreg[s].z, p[u][s], o[u][2], 0, 0, 0);
+          o[u][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vreg[s].w, p[u][s], o[u][3], 0, 0, 0);
+        }
       }
   };
 
@@ -403,10 +434,10 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
 #pragma unroll
       for (int v4 = 0; v4 < 4; ++v4) {
         const float4 x = *reinterpret_cast<const float4*>(&s_q[j][16 * g + 4 * v4]);
-        qreg[4 * v4 + 0] = x.x * qscale;
-        qreg[4 * v4 + 1] = x.y * qscale;
-        qreg[4 * v4 + 2] = x.z * qscale;
-        qreg[4 * v4 + 3] = x.w * qscale;
+        qreg[0][4 * v4 + 0] = x.x * qscale;
+        qreg[0][4 * v4 + 1] = x.y * qscale;
+        qreg[0][4 * v4 + 2] = x.z * qscale;
+        qreg[0][4 * v4 + 3] = x.w * qscale;
       }
     }
     if (any) {
@@ -456,17 +487,23 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
     }
   }
 
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
-  if constexpr (KS == 1) {
-    if (q_ok) {
-      const float inv = 1.f / l;
-      float* op = a.out + (int64_t)(row0 + qi) * a.out_stride + h * kHeadDim + 16 * g;
-      // o[t][r] = O^T[dim-row 4g + r][query j] = output dim 16g + 4r + t.
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        *reinterpret_cast<float4*>(op + 4 * r) =
-            make_float4(o[0][r] * inv, o[1][r] * inv, o[2][r] * inv, o[3][r] * inv);
+  for (int u = 0; u < QH; ++u) {
+    l[u] += __shfl_xor(l[u], 16);
+    l[u] += __shfl_xor(l[u], 32);
+  }
+  if constexpr (KS == 1) {
+#pragma unroll
+    for (int u = 0; u < QH; ++u) {
+      if (q_ok[u]) {
+        const float inv = 1.f / l[u];
+        float* op = a.out + (int64_t)(row0 + qi + 16 * u) * a.out_stride + h * kHeadDim + 16 * g;
+        // o[u][t][r] = O^T[dim-row 4g + r][query j] = output dim 16g + 4r + t.
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          *reinterpret_cast<float4*>(op + 4 * r) =
+              make_float4(o[u][0][r] * inv, o[u][1][r] * inv, o[u][2][r] * inv, o[u][3][r] * inv);
+      }
     }
   } else {
     // Merge the KS partial states (m, l, O) per query through LDS. Lane (j, g) of
@@ -477,10 +514,10 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
 #pragma unroll
     for (int r = 0; r < 4; ++r)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) s_o[wave][lane][4 * r + t] = o[t][r];
+      for (int t = 0; t < 4; ++t) s_o[wave][lane][4 * r + t] = o[0][t][r];
     if (g == 0) {
-      s_ml[wave][0][j] = m;
-      s_ml[wave][1][j] = l;
+      s_ml[wave][0][j] = m[0];
+      s_ml[wave][1][j] = l[0];
     }
     __syncthreads();
     // Thread (wave w, lane) finishes dims 16g + 4w' .. +3 of query j for w' = w, w + KS, ... < 4.
@@ -500,7 +537,7 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
         acc.z = fmaf(s_o[w][lane][4 * part + 2], cw, acc.z);
         acc.w = fmaf(s_o[w][lane][4 * part + 3], cw, acc.w);
       }
-      if (q_ok) {
+      if (q_ok[0]) {
         const float inv = 1.f / L;
         float* op = a.out + (int64_t)(row0 + qi) * a.out_stride + h * kHeadDim + 16 * g + 4 * part;
         *reinterpret_cast<float4*>(op) = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
@@ -509,9 +546,9 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
   }
 }
 
-template <int BS_CT, int KS>
+template <int BS_CT, int KS, int QH = 1>
 __global__ __launch_bounds__(kWave* KS) void prefill_kernel(const PrefillArgs a) {
-  prefill_workgroup<BS_CT, KS>(a, blockIdx.x);
+  prefill_workgroup<BS_CT, KS, QH>(a, blockIdx.x);
 }
 
 // The 8-wave instance reserves this much extra (unused) LDS per workgroup so that a
@@ -521,14 +558,14 @@ __global__ __launch_bounds__(kWave* KS) void prefill_kernel(const PrefillArgs a)
 // tail chunk with 5 / 102 / 9 rows at position 768: 22.2 -> 14.5 us.
 constexpr size_t kLdsOneGroupPerCu = 64 * 1024;
 
-template <int BS_CT, int KS>
+template <int BS_CT, int KS, int QH = 1>
 void launch_prefill_ks(const PrefillArgs& a, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   const size_t lds = KS == 8 ? kLdsOneGroupPerCu : 0;
   if (start == nullptr && stop == nullptr)
-    hipLaunchKernelGGL((prefill_kernel<BS_CT, KS>), dim3((unsigned)a.total), dim3(kWave * KS), lds, stream, a);
+    hipLaunchKernelGGL((prefill_kernel<BS_CT, KS, QH>), dim3((unsigned)a.total), dim3(kWave * KS), lds, stream, a);
   else
-    hipExtLaunchKernelGGL((prefill_kernel<BS_CT, KS>), dim3((unsigned)a.total), dim3(kWave * KS), lds, stream, start,
-                          stop, 0, a);
+    hipExtLaunchKernelGGL((prefill_kernel<BS_CT, KS, QH>), dim3((unsigned)a.total), dim3(kWave * KS), lds, stream,
+                          start, stop, 0, a);
 }
 
 // Waves per workgroup: the largest key split KS that still lets every workgroup of
@@ -547,10 +584,30 @@ int choose_key_split(int64_t tiles) {
   return 1;
 }
 
+// Row tiles (heads x ceil(rows / 16)) from which a one-wave launch gives each wave two query
+// tiles: two rounds of 4 waves per SIMD of the 256 CUs before halving the wave count. (At
+// 4,608 row tiles of 256-row prompts two tiles per wave ran 5 % slower, at 6,144 of 512-row
+// prompts 3.5 % faster.)
+constexpr int64_t kTwoTileMinTiles = 8192;
+
 template <int BS_CT>
 void launch_prefill(const PrefillArgs& a, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   switch (choose_key_split((int64_t)a.groups * a.qtiles)) {
-    case 1: launch_prefill_ks<BS_CT, 1>(a, stream, start, stop); break;
+    case 1:
+      if (BS_CT == kTile && (int64_t)a.num_heads * ((a.num_q_rows + kTile - 1) / kTile) >= kTwoTileMinTiles) {
+        // More tiles than the key split pays for, and many rows: with block size 16 each wave
+        // takes two consecutive query tiles, so every key tile's loads feed both and the wave has
+        // two independent softmax chains (per launch: 32 prompts U[256,1024] 248 -> 233 us,
+        // 64 prompts x 300 138.6 -> 114.9; 15 prompts U[16,256], 1,530 row tiles, went
+        // 21.2 -> 28.1, hence the row bound).
+        PrefillArgs a2 = a;
+        a2.qtiles = (a.qtiles + 1) / 2;
+        a2.total = kXcds * ((a.groups + kXcds - 1) / kXcds) * a2.qtiles;
+        if constexpr (BS_CT == kTile) launch_prefill_ks<BS_CT, 1, 2>(a2, stream, start, stop);
+      } else {
+        launch_prefill_ks<BS_CT, 1>(a, stream, start, stop);
+      }
+      break;
     case 2: launch_prefill_ks<BS_CT, 2>(a, stream, start, stop); break;
     case 4: launch_prefill_ks<BS_CT, 4>(a, stream, start, stop); break;
     default: launch_prefill_ks<BS_CT, 8>(a, stream, start, stop); break;
