@@ -263,6 +263,51 @@ def decode_op_alone(seed: int = 2) -> dict:
             "us_per_call_host_paced": round(us_paced, 2)}  # fmt: skip
 
 
+def prefill_batch(seed: int = 32, reps: int = 3) -> dict:
+    """The prefill kernel on a large launch, as the engine's prefill steps run it: one prefill step of
+    32 prompts of U[256,1024] random tokens (block size 16) through the model, every layer's
+    tq_paged_prefill launch timed by the events it records; causal-exact flops over the launch time
+    against the fp32 MFMA peak. The step runs reps times from the same state (its cache writes are the
+    same each time); the median per layer over all runs."""
+    import torch
+
+    from tokquay_amd import kv_cache
+    from tokquay_amd.generate import paged_forward
+    from tokquay_amd.kv_cache import BlockAllocator
+    from tokquay_amd.sequence import Sequence
+
+    model = load_model()
+    alloc = BlockAllocator(model.cfg, 4096, BLOCK, device="cuda")
+    rng = random.Random(seed)
+    seqs = [Sequence(i, [rng.randrange(50256) for _ in range(rng.randint(256, 1024))]) for i in range(32)]
+    for sq in seqs:
+        alloc.allocate(sq)
+    lens = [sq.num_tokens for sq in seqs]
+    flops = prefill_flops([0] * len(lens), lens)
+    paged_forward(model, alloc, seqs)  # warm-up
+    times = []
+    try:
+        for _ in range(reps):
+            for sq in seqs:
+                sq.num_cached_tokens = 0
+            timer = LaunchTimer("prefill")
+            kv_cache.PagedBatch.launch_hook = timer
+            paged_forward(model, alloc, seqs)
+            torch.cuda.synchronize()
+            kv_cache.PagedBatch.launch_hook = None
+            times += [a.elapsed_time(b) * 1e3 for a, b in timer.pairs["prefill"]]
+    finally:
+        kv_cache.PagedBatch.launch_hook = None
+    alloc.check_device_errors()
+    us = statistics.median(times)
+    return {"workload": f"one prefill step: 32 prompts U[256,1024] at start 0 ({sum(lens)} rows), block 16, "
+                        "12 layers; median launch over the layers of 3 runs",
+            "kernel": "tq_paged_prefill (fp32 MFMA 16x16x4; one wave per workgroup, two query tiles per wave)",
+            "bound": "mfma", "us_per_launch": round(us, 2), "mflop_per_launch": round(flops / 1e6, 1),
+            "achieved": round(flops / us / 1e6, 2), "peak": MFMA_FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(flops / us / 1e6 / MFMA_FP32_PEAK_TFLOPS, 4)}  # fmt: skip
+
+
 def mixed_chunked_step(seed: int = 5) -> tuple[dict, dict]:
     """Mixed chunked-prefill + decode steps: 4 prompts of U[512,1024] random tokens fed in 256-token
     chunks (chunk k starts at 256k) next to 128 sequences decoding at context U[64,768], block size 16.
@@ -925,6 +970,10 @@ def main() -> int:
         log(f"prefill: {result['prefill']['achieved']} TFLOP/s = {result['prefill']['frac']:.3f} of fp32 MFMA peak; "
             f"mixed launch: {result['mixed_attention']['frac']:.3f} of its combined roofline "
             f"({result['mixed_attention']['two_launch_frac']:.3f} as two launches)")
+        log("prefill batch (32 prompts U[256,1024]) ...")
+        result["prefill_batch"] = prefill_batch()
+        log(f"prefill batch: {result['prefill_batch']['us_per_launch']} us per launch = "
+            f"{result['prefill_batch']['frac']:.3f} of fp32 MFMA peak")
         result["mixed_engine"] = [mixed_engine(chunked=True), mixed_engine(chunked=False)]
         torch.cuda.empty_cache()
     if not args.no_itl:
