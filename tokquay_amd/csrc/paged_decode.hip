@@ -159,24 +159,27 @@ int num_partitions(int32_t max_context_len, int part) {
 }
 
 // Waves per (sequence, head) workgroup of the split kernel, or 0 for the one-wave-per-partition
-// grid. The larger of two widths, each a power of two:
+// grid. The largest of three widths, each a power of two:
 // * parallelism: where the automatic partitioning would split sequences (small batches), its
-//   partition count (at most 16), so the same parallelism needs no partials and no merge launch
-//   (8 sequences, contexts 300-500: 12.4 -> ... us per layer);
+//   partition count, at most 8, so the same parallelism needs no partials and no merge launch
+//   (8 sequences, contexts 300-500: 12.4 -> ... us per layer; 8 waves rather than 16 at 4 / 8 / 16
+//   sequences 8.3 -> 7.8, 8.8 -> 8.3, 15.5 -> 14.8 us, one sequence 5.8 either way);
 // * length balance: about 128 positions per wave for the longest context (2 to 8 waves). Short
 //   waves end the launch evenly: with one wave per (sequence, head) the longest contexts form its
 //   tail. Measured per launch against the one-wave grid (queued launches, 12-layer pool):
 //   256 sequences at U[256,1024] 161.3 -> 157.4 us, U[64,512] 76.7 -> 75.3, U[16,256] 40.3 -> 39.2;
 //   128 at U[64,768] 57.0 -> 54.7, U[1024,2048] 193.8 -> 186.2 (8 waves against 2).
+// * long contexts: at most 1024 positions per wave (16 waves up to 16,384 positions).
 // Contexts of at most 128 positions keep one wave per (sequence, head) unless the batch is small.
-// Explicit partition sizes keep the partition grid.
+// Beyond 16,384 positions, and with explicit partition sizes, the partition grid runs.
 int split_waves(int32_t num_seqs, int32_t num_heads, int32_t max_context_len, int32_t requested) {
   if (requested > 0 || max_context_len <= 0) return 0;
   const int parts = num_partitions(max_context_len, choose_partition(num_seqs, num_heads, max_context_len, 0));
   int w = 1;
-  while (w < parts && w < 16) w *= 2;
+  while (w < parts && w < 8) w *= 2;
   if (max_context_len > 128)
     while (w < 8 && (int64_t)w * 128 < max_context_len) w *= 2;
+  while (w < 16 && (int64_t)w * kMaxPartition < max_context_len) w *= 2;
   if (w < 2) return 0;
   return (int64_t)max_context_len <= (int64_t)w * kMaxPartition ? w : 0;
 }
