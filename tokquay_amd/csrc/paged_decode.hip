@@ -177,6 +177,10 @@ int split_waves(int32_t num_seqs, int32_t num_heads, int32_t max_context_len, in
   const int parts = num_partitions(max_context_len, choose_partition(num_seqs, num_heads, max_context_len, 0));
   int w = 1;
   while (w < parts && w < 8) w *= 2;
+  // ... and about six waves per SIMD over the launch while each wave keeps ~64 positions (64
+  // sequences at U[16,512]: 20.6 -> 20.1 us with 8 waves; 256 at U[1,128]: 21.5 -> 20.8 with 2).
+  const int64_t pairs = (int64_t)num_seqs * num_heads;
+  while (w < 8 && pairs * w < 6144 && (int64_t)w * 64 < max_context_len) w *= 2;
   if (max_context_len > 128)
     while (w < 8 && (int64_t)w * 128 < max_context_len) w *= 2;
   while (w < 16 && (int64_t)w * kMaxPartition < max_context_len) w *= 2;
