@@ -17,9 +17,13 @@
 // group g supplies k = kb + 4 g + j to both operands. The accumulator's lane (j, g)
 // holds Y^T[n0 + 4 g + r][m = 16 mb + j], r = 0..3.
 //
-// Work split: a wave owns one 192-wide k slice (each lane keeps its part of X in 12
-// float4 registers per row block) of 16 R output columns; a workgroup's four waves
+// Work split: a wave owns one 96-wide k slice (each lane keeps its part of X in 6
+// float4 registers per row block) of 16 R output columns; a workgroup's eight waves
 // cover 768 of K, and their partial products are summed through LDS in a fixed order.
+// Eight waves of 96 beat four of 192 (same bytes in flight per workgroup, half the
+// registers per wave, so twice the waves resident): weights evicted before each call,
+// GPT-2's four projections at 1-16 rows 0-3 % faster, at 32 rows 5-10 %; the LM head
+// with argmax at 1 / 8 / 16 rows 46.6 / 50.0 / 52.9 -> 44.4 / 45.5 / 47.2 us.
 // Up to 16 rows are one row block; 17-64 rows run as row groups of two blocks, one
 // workgroup per (row group, column block). Every load of W is issued before anything
 // waits: the first two column blocks at the start, block r + 2 as soon as block r's
@@ -43,6 +47,9 @@
 //
 // Reference semantics: nn.Linear (tokquay/model.py:62-63, :103-104), LayerNorm
 // (:117-118, :145), tied LM head (:180).
+
+#include <algorithm>
+#include <mutex>
 
 #include "tq_internal.h"
 
@@ -69,6 +76,7 @@ struct SkinnyArgs {
   float* partials;    // [blocks][KSPLIT][16][16 R] (split launches)
   int32_t* arrivals;  // [blocks], zero between launches (split launches)
   uint64_t* keys;     // [M][column blocks] candidates of each 32-column slice (argmax launches)
+  int32_t col_blocks; // column blocks of an argmax launch (its workgroups loop over them)
   float eps;
   int32_t M;
   int32_t N;
@@ -103,7 +111,11 @@ __global__ __launch_bounds__(kWave* KW) void skinny_linear_kernel(const SkinnyAr
   const int i = lane & 15;
   const int g = lane >> 4;
   const int k_lo = (blockIdx.y * KW + wave) * kRange;  // blockIdx.y: the K part (split launches)
-  const int n_base = blockIdx.x * (16 * R);
+  // The column block: blockIdx.x, or for argmax launches (a grid of as many workgroups as fit at
+  // once) blockIdx.x, blockIdx.x + gridDim.x, ..., each workgroup keeping its X slice and
+  // LayerNorm across them and loading a block's weights while it reduces the one before.
+  int cb_cur = blockIdx.x;
+  int n_base = cb_cur * (16 * R);
   const int row0 = blockIdx.z * kRows;              // blockIdx.z: the row group (more than kRows rows)
   const int M = min(a.M - row0, kRows);             // rows of this workgroup
   const int cb = blockIdx.z * gridDim.x + blockIdx.x;  // (row group, column block): its split workspace
@@ -206,124 +218,168 @@ __global__ __launch_bounds__(kWave* KW) void skinny_linear_kernel(const SkinnyAr
 
   // Each W float4 feeds the MB row blocks' MFMAs (independent accumulators).
   floatx4 acc[R][MB];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const floatx4(&wv)[T] = wb[r & 1];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) acc[r][mb] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) acc[r][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][0], xr[mb][t].x, acc[r][mb], 0, 0, 0);
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) acc[r][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][1], xr[mb][t].y, acc[r][mb], 0, 0, 0);
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) acc[r][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][2], xr[mb][t].z, acc[r][mb], 0, 0, 0);
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) acc[r][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][3], xr[mb][t].w, acc[r][mb], 0, 0, 0);
-    }
-    if (r + 2 < R) {  // block r + 2 into the registers block r just freed
-      __builtin_amdgcn_sched_barrier(0);
-      load_w(wb[r & 1], r + 2);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  }
-
-  // Partial products of the KW waves: part[w][r][mb][lane][reg], 5 floats per lane (bank spread).
   __shared__ float part[KW][R][MB][kWave][5];
+  for (;;) {
+    const int n_cur = cb_cur * (16 * R);
 #pragma unroll
-  for (int r = 0; r < R; ++r)
+    for (int r = 0; r < R; ++r) {
+      const floatx4(&wv)[T] = wb[r & 1];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+      for (int mb = 0; mb < MB; ++mb) acc[r][mb] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int q = 0; q < 4; ++q) part[wave][r][mb][lane][q] = acc[r][mb][q];
-  __syncthreads();
-
-  // Output o = (m, nn): m = o / (16 R), column n_base + nn. Its value sits in row block m / 16,
-  // lane m % 16 + 16 (c / 4), register c % 4 of column block nn / 16, c = nn % 16.
-  constexpr int kOut = 16 * R * kRows;
-  auto gather = [&](int m, int nn) {
-    const int c = nn & 15;
-    float v = 0.f;
+      for (int t = 0; t < T; ++t) {
 #pragma unroll
-    for (int w = 0; w < KW; ++w) v += part[w][nn >> 4][m >> 4][(m & 15) + 16 * (c >> 2)][c & 3];
-    return v;
-  };
-  if constexpr (EPI == kEpiArgmax) {
-    // Greedy ids instead of logits. Row m's 16 R = 32 columns of this workgroup sit in 32
-    // consecutive threads (one half wave), reduced with shuffles to one key, which the half
-    // wave's first lane stores as this column slice's candidate for row m; argmax_keys_kernel
-    // reduces the slices' candidates per row right after. (Folding them into per-row maxima
-    // with atomics, the last workgroup writing the ids, serialised ~1,571 RMWs per row on a few
-    // addresses: 8 rows 0.45 -> 0.49 ms per decode step, 0.46 with a load before each RMW.)
-    static_assert(KSPLIT == 1 && MB == 1 && 16 * R == 32 && kOut % (kWave * KW) == 0,
-                  "argmax launches: one row block, 32 columns per workgroup, whole half waves per row");
+        for (int mb = 0; mb < MB; ++mb) acc[r][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][0], xr[mb][t].x, acc[r][mb], 0, 0, 0);
 #pragma unroll
-    for (int o0 = 0; o0 < kOut; o0 += kWave * KW) {  // the same trip count for every thread
-      const int o = o0 + threadIdx.x;
-      const int m = o / 32;
-      const int nn = o - 32 * m;
-      const int n = n_base + nn;
-      uint64_t key = 0;  // no candidate: columns past N
-      if (m < M && n < a.N) {
-        float v = gather(m, nn);
-        if (a.bias != nullptr) v += a.bias[n];
-        key = argmax_key(v, (uint32_t)n);
+        for (int mb = 0; mb < MB; ++mb) acc[r][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][1], xr[mb][t].y, acc[r][mb], 0, 0, 0);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[r][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][2], xr[mb][t].z, acc[r][mb], 0, 0, 0);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[r][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[t][3], xr[mb][t].w, acc[r][mb], 0, 0, 0);
       }
+      if (r + 2 < R) {  // block r + 2 into the registers block r just freed
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(wb[r & 1], r + 2);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    int cb_next = -1;
+    if constexpr (EPI == kEpiArgmax) {
+      cb_next = cb_cur + (int)gridDim.x;  // wave-uniform
+      if (cb_next < a.col_blocks) {  // the next block's weights into the registers just freed
+        n_base = cb_next * (16 * R);
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(wb[0], 0);
+        load_w(wb[1], 1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+
+    // Partial products of the KW waves: part[w][r][mb][lane][reg], 5 floats per lane (bank spread).
 #pragma unroll
-      for (int off = 16; off > 0; off >>= 1) key = max_u64(key, __shfl_xor(key, off));
-      if (nn == 0 && m < M) a.keys[(int64_t)m * gridDim.x + blockIdx.x] = key;
-    }
-  } else if constexpr (KSPLIT == 1) {
-    for (int o = threadIdx.x; o < kOut; o += kWave * KW) {
-      const int m = o / (16 * R);
-      const int nn = o - m * (16 * R);
-      const int n = n_base + nn;
-      if (m >= M || n >= a.N) continue;
-      store_output<EPI>(a, row0 + m, n, gather(m, nn));
-    }
-  } else {
-    float* mine = a.partials + ((int64_t)cb * KSPLIT + blockIdx.y) * kOut;
-    for (int o = threadIdx.x; o < kOut; o += kWave * KW) {
-      const int m = o / (16 * R);
-      if (m >= M) break;  // rows past the batch are never read
-      const int nn = o - m * (16 * R);
-      __hip_atomic_store(mine + o, gather(m, nn), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    // Ordering, as the compiler implements agent-scope release / acquire on gfx942 / gfx950 (LLVM
-    // AMDGPUUsage memory model) minus the cache maintenance only non-atomic accesses need:
-    // the tile stores are agent-scope atomic stores (global_store sc1: written through to the
-    // device coherence point, nothing left dirty in the XCD's L2, so no buffer_wbl2), and every
-    // wave waits for their completion (s_waitcnt vmcnt(0)) before the barrier, so they are
-    // performed at agent scope before thread 0's counter RMW is issued. The last arriver's tile
-    // loads are agent-scope atomic loads (global_load sc1: never served by a stale L1 / L2 line,
-    // so no buffer_inv), issued after the RMW returned (its value goes through LDS and a
-    // barrier). A release / acquire RMW instead (buffer_wbl2 sc1 + buffer_inv sc1 per workgroup,
-    // plain tile accesses) gave identical bits and cost 2.1 us per launch at 8 rows (6.5 -> 8.6 us),
-    // 7.6 us at 64 rows.
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
-    __syncthreads();                // ... and every thread's
-    __shared__ int s_last;
-    if (threadIdx.x == 0)
-      s_last = __hip_atomic_fetch_add(a.arrivals + cb, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-               KSPLIT - 1;
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) part[wave][r][mb][lane][q] = acc[r][mb][q];
     __syncthreads();
-    if (!s_last) return;
-    const float* tiles = a.partials + (int64_t)cb * KSPLIT * kOut;
-    for (int o = threadIdx.x; o < kOut; o += kWave * KW) {
-      const int m = o / (16 * R);
-      if (m >= M) break;
-      const int nn = o - m * (16 * R);
-      const int n = n_base + nn;
-      if (n >= a.N) continue;
+
+    // Output o = (m, nn): m = o / (16 R), column n_base + nn. Its value sits in row block m / 16,
+    // lane m % 16 + 16 (c / 4), register c % 4 of column block nn / 16, c = nn % 16.
+    constexpr int kOut = 16 * R * kRows;
+    auto gather = [&](int m, int nn) {
+      const int c = nn & 15;
       float v = 0.f;
 #pragma unroll
-      for (int ks = 0; ks < KSPLIT; ++ks)
-        v += __hip_atomic_load(tiles + ks * kOut + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      store_output<EPI>(a, row0 + m, n, v);
+      for (int w = 0; w < KW; ++w) v += part[w][nn >> 4][m >> 4][(m & 15) + 16 * (c >> 2)][c & 3];
+      return v;
+    };
+    if constexpr (EPI == kEpiArgmax) {
+      // Greedy ids instead of logits. Row m's 16 R = 32 columns of this workgroup sit in 32
+      // consecutive threads (one half wave), reduced with shuffles to one key, which the half
+      // wave's first lane stores as this column slice's candidate for row m; argmax_keys_kernel
+      // reduces the slices' candidates per row right after. (Folding them into per-row maxima
+      // with atomics, the last workgroup writing the ids, serialised ~1,571 RMWs per row on a few
+      // addresses: 8 rows 0.45 -> 0.49 ms per decode step, 0.46 with a load before each RMW.)
+      static_assert(KSPLIT == 1 && MB == 1 && 16 * R == 32 && kOut % (kWave * KW) == 0,
+                    "argmax launches: one row block, 32 columns per workgroup, whole half waves per row");
+#pragma unroll
+      for (int o0 = 0; o0 < kOut; o0 += kWave * KW) {  // the same trip count for every thread
+        const int o = o0 + threadIdx.x;
+        const int m = o / 32;
+        const int nn = o - 32 * m;
+        const int n = n_cur + nn;
+        uint64_t key = 0;  // no candidate: columns past N
+        if (m < M && n < a.N) {
+          float v = gather(m, nn);
+          if (a.bias != nullptr) v += a.bias[n];
+          key = argmax_key(v, (uint32_t)n);
+        }
+#pragma unroll
+        for (int off = 16; off > 0; off >>= 1) key = max_u64(key, __shfl_xor(key, off));
+        if (nn == 0 && m < M) a.keys[(int64_t)m * a.col_blocks + cb_cur] = key;
+      }
+      if (cb_next >= a.col_blocks) return;
+      __syncthreads();  // every wave has read part before the next block overwrites it
+      cb_cur = cb_next;
+      continue;
+    } else if constexpr (KSPLIT == 1) {
+      for (int o = threadIdx.x; o < kOut; o += kWave * KW) {
+        const int m = o / (16 * R);
+        const int nn = o - m * (16 * R);
+        const int n = n_base + nn;
+        if (m >= M || n >= a.N) continue;
+        store_output<EPI>(a, row0 + m, n, gather(m, nn));
+      }
+    } else {
+      float* mine = a.partials + ((int64_t)cb * KSPLIT + blockIdx.y) * kOut;
+      for (int o = threadIdx.x; o < kOut; o += kWave * KW) {
+        const int m = o / (16 * R);
+        if (m >= M) break;  // rows past the batch are never read
+        const int nn = o - m * (16 * R);
+        __hip_atomic_store(mine + o, gather(m, nn), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      // Ordering, as the compiler implements agent-scope release / acquire on gfx942 / gfx950 (LLVM
+      // AMDGPUUsage memory model) minus the cache maintenance only non-atomic accesses need:
+      // the tile stores are agent-scope atomic stores (global_store sc1: written through to the
+      // device coherence point, nothing left dirty in the XCD's L2, so no buffer_wbl2), and every
+      // wave waits for their completion (s_waitcnt vmcnt(0)) before the barrier, so they are
+      // performed at agent scope before thread 0's counter RMW is issued. The last arriver's tile
+      // loads are agent-scope atomic loads (global_load sc1: never served by a stale L1 / L2 line,
+      // so no buffer_inv), issued after the RMW returned (its value goes through LDS and a
+      // barrier). A release / acquire RMW instead (buffer_wbl2 sc1 + buffer_inv sc1 per workgroup,
+      // plain tile accesses) gave identical bits and cost 2.1 us per launch at 8 rows (6.5 -> 8.6 us),
+      // 7.6 us at 64 rows.
+      __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
+      __syncthreads();                // ... and every thread's
+      __shared__ int s_last;
+      if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(a.arrivals + cb, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 KSPLIT - 1;
+      __syncthreads();
+      if (!s_last) return;
+      const float* tiles = a.partials + (int64_t)cb * KSPLIT * kOut;
+      for (int o = threadIdx.x; o < kOut; o += kWave * KW) {
+        const int m = o / (16 * R);
+        if (m >= M) break;
+        const int nn = o - m * (16 * R);
+        const int n = n_base + nn;
+        if (n >= a.N) continue;
+        float v = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < KSPLIT; ++ks)
+          v += __hip_atomic_load(tiles + ks * kOut + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        store_output<EPI>(a, row0 + m, n, v);
+      }
+      if (threadIdx.x == 0) __hip_atomic_store(a.arrivals + cb, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (threadIdx.x == 0) __hip_atomic_store(a.arrivals + cb, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    break;  // other launches: one column block per workgroup
   }
+}
+
+// Workgroups of `kernel` the device holds at once (its occupancy per CU times the CUs), cached per
+// (device, kernel); one per CU if the runtime cannot say.
+int resident_groups(const void* kernel, int block_threads) {
+  struct Entry {
+    int device;
+    const void* kernel;
+    int groups;
+  };
+  static Entry cache[32];
+  static int used = 0;
+  static std::mutex mu;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < used; ++i)
+    if (cache[i].device == dev && cache[i].kernel == kernel) return cache[i].groups;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block_threads, 0) != hipSuccess || per_cu < 1)
+    per_cu = 1;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
+  const int groups = per_cu * cus;
+  if (used < 32) cache[used++] = {dev, kernel, groups};
+  return groups;
 }
 
 template <int T, int KW, int R, int MB, bool LN, int KSPLIT>
@@ -333,8 +389,15 @@ void launch_skinny_epi(const SkinnyArgs& a, int epi, hipStream_t s) {
   const dim3 block(kWave * KW);
   switch (epi) {
     case kEpiArgmax:
-      if constexpr (R == 2 && MB == 1 && KSPLIT == 1)
-        hipLaunchKernelGGL((skinny_linear_kernel<T, KW, R, MB, LN, kEpiArgmax, KSPLIT>), grid, block, 0, s, a);
+      // As many workgroups as the device holds at once, each looping over column blocks: with
+      // one workgroup per block the LM head's 1,571 blocks took four rounds of 512 resident
+      // workgroups (184 VGPRs), the last one nearly empty, and each round normalised X again.
+      if constexpr (R == 2 && MB == 1 && KSPLIT == 1) {
+        const void* kern = reinterpret_cast<const void*>(&skinny_linear_kernel<T, KW, R, MB, LN, kEpiArgmax, KSPLIT>);
+        const int groups = std::min(a.col_blocks, resident_groups(kern, kWave * KW));
+        hipLaunchKernelGGL((skinny_linear_kernel<T, KW, R, MB, LN, kEpiArgmax, KSPLIT>), dim3((unsigned)groups), block,
+                           0, s, a);
+      }
       break;
     case kEpiGelu:
       hipLaunchKernelGGL((skinny_linear_kernel<T, KW, R, MB, LN, kEpiGelu, KSPLIT>), grid, block, 0, s, a);
@@ -348,15 +411,15 @@ void launch_skinny_epi(const SkinnyArgs& a, int epi, hipStream_t s) {
   }
 }
 
-// A wave keeps a 192-wide k slice of X in registers: 12 float4 per row block. Up to 16 rows run
+// A wave keeps a 96-wide k slice of X in registers: 6 float4 per row block. Up to 16 rows run
 // as one row block; more as row groups of two blocks (32 rows), one workgroup per (row group,
 // column block), each reading its columns of W (the second read of a column mostly hits the
 // memory-side cache). Four row blocks in one workgroup (96-wide slices, eight waves) left 112
 // of the 256 CUs idle at 2,304 columns and lost to this.
 template <int R, bool LN, int KSPLIT>
 void launch_skinny_rows(const SkinnyArgs& a, int epi, hipStream_t s) {
-  if (a.M <= kSkinnyRows) launch_skinny_epi<12, 4, R, 1, LN, KSPLIT>(a, epi, s);
-  else launch_skinny_epi<12, 4, R, 2, LN, KSPLIT>(a, epi, s);
+  if (a.M <= kSkinnyRows) launch_skinny_epi<6, 8, R, 1, LN, KSPLIT>(a, epi, s);
+  else launch_skinny_epi<6, 8, R, 2, LN, KSPLIT>(a, epi, s);
 }
 
 // Launch shape for (N, K, LN): column blocks per workgroup, workgroups per column block (K
@@ -542,9 +605,10 @@ extern "C" tq_status tq_skinny_linear_argmax(int64_t* ids, const float* x, int64
   a.N = N;
   a.K = K;
   a.keys = static_cast<uint64_t*>(workspace);  // [M][slices]: every entry read is written first
+  a.col_blocks = (int32_t)skinny_argmax_slices(N);
   hipStream_t s = (hipStream_t)stream;
-  if (ln_gamma != nullptr) launch_skinny_epi<12, 4, 2, 1, true, 1>(a, kEpiArgmax, s);
-  else launch_skinny_epi<12, 4, 2, 1, false, 1>(a, kEpiArgmax, s);
+  if (ln_gamma != nullptr) launch_skinny_epi<6, 8, 2, 1, true, 1>(a, kEpiArgmax, s);
+  else launch_skinny_epi<6, 8, 2, 1, false, 1>(a, kEpiArgmax, s);
   hipLaunchKernelGGL(argmax_keys_kernel, dim3((unsigned)M), dim3(256), 0, s, a.keys,
                      (int32_t)skinny_argmax_slices(N), ids);
   return check_launch();
