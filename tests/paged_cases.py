@@ -26,9 +26,10 @@ C = H * D
 RTOL, ATOL = 1e-5, 1e-4  # fp32 attention outputs vs the reference gather path
 
 
-def garbage_pool(num_blocks: int, n_layer: int, block_size: int, seed: int, scale: float = 50.0) -> torch.Tensor:
+def garbage_pool(num_blocks: int, n_layer: int, block_size: int, seed: int, scale: float = 50.0,
+                 n_head: int = H) -> torch.Tensor:
     g = torch.Generator().manual_seed(seed)
-    return torch.randn(num_blocks, n_layer, 2, H, block_size, D, generator=g) * scale
+    return torch.randn(num_blocks, n_layer, 2, n_head, block_size, D, generator=g) * scale
 
 
 def deal_tables(num_blocks: int, ctxs: list[int], block_size: int, seed: int) -> list[list[int]]:
@@ -44,13 +45,14 @@ def deal_tables(num_blocks: int, ctxs: list[int], block_size: int, seed: int) ->
 
 
 class Scenario:
-    def __init__(self, starts, new_lens, block_size=16, n_layer=1, layer=0, num_blocks=None, seed=0):
+    def __init__(self, starts, new_lens, block_size=16, n_layer=1, layer=0, num_blocks=None, seed=0, n_head=H):
+        self.H, self.C = n_head, n_head * D
         self.starts, self.new_lens = list(starts), list(new_lens)
         self.block_size, self.n_layer, self.layer = block_size, n_layer, layer
         self.ctxs = [s + n for s, n in zip(self.starts, self.new_lens)]
         need = sum(cdiv(c, block_size) for c in self.ctxs)
         self.num_blocks = num_blocks or need + 3
-        self.pool = garbage_pool(self.num_blocks, n_layer, block_size, seed)
+        self.pool = garbage_pool(self.num_blocks, n_layer, block_size, seed, n_head=n_head)
         self.tables = deal_tables(self.num_blocks, self.ctxs, block_size, seed + 1)
         g = torch.Generator().manual_seed(seed + 2)
         # History: K/V of the positions already cached, written straight into their slots.
@@ -61,11 +63,11 @@ class Scenario:
                 off.append(p % block_size)
         if blk:
             blk_t, off_t = torch.tensor(blk), torch.tensor(off)
-            self.pool[blk_t, layer, 0, :, off_t] = torch.randn(len(blk), H, D, generator=g)
-            self.pool[blk_t, layer, 1, :, off_t] = torch.randn(len(blk), H, D, generator=g)
+            self.pool[blk_t, layer, 0, :, off_t] = torch.randn(len(blk), n_head, D, generator=g)
+            self.pool[blk_t, layer, 1, :, off_t] = torch.randn(len(blk), n_head, D, generator=g)
         B, T = len(self.starts), max(self.new_lens)
         # New tokens, [B, H, T, d]; padded columns hold huge values so a stray write or read shows.
-        self.q, self.k, self.v = (torch.randn(B, H, T, D, generator=g) for _ in range(3))
+        self.q, self.k, self.v = (torch.randn(B, n_head, T, D, generator=g) for _ in range(3))
         for b, n in enumerate(self.new_lens):
             for t in (self.q, self.k, self.v):
                 t[b, :, n:] = 1e4
@@ -90,7 +92,7 @@ class Scenario:
             vals = pool_after[blocks, self.layer, 1, :, offs].double().numpy()
             out = np.stack(
                 [brute_force_attention(self.q[b, h, :n].double().numpy(), keys[:, h], vals[:, h], 1 / math.sqrt(D))
-                 for h in range(H)],
+                 for h in range(self.H)],
                 axis=1,
             )  # fmt: skip
             res.append(out)
@@ -99,8 +101,8 @@ class Scenario:
     # ---- product ----------------------------------------------------------------------
     def packed_qkv(self, token_index: torch.Tensor) -> torch.Tensor:
         B, _, T, _ = self.q.shape
-        qkv = torch.cat([t.transpose(1, 2).reshape(B, T, C) for t in (self.q, self.k, self.v)], dim=-1)
-        return qkv.reshape(B * T, 3 * C).index_select(0, token_index.cpu())
+        qkv = torch.cat([t.transpose(1, 2).reshape(B, T, self.C) for t in (self.q, self.k, self.v)], dim=-1)
+        return qkv.reshape(B * T, 3 * self.C).index_select(0, token_index.cpu())
 
     def run_product(self, partition_tokens: int = 0):
         """(pool after attend, packed output ``[N, C]``, the PagedBatch) from the HIP path."""
@@ -118,4 +120,4 @@ class Scenario:
 
     def packed_reference(self, out_ref: torch.Tensor, token_index: torch.Tensor) -> torch.Tensor:
         B, _, T, _ = out_ref.shape
-        return out_ref.transpose(1, 2).reshape(B * T, C).index_select(0, token_index.cpu())
+        return out_ref.transpose(1, 2).reshape(B * T, self.C).index_select(0, token_index.cpu())

@@ -28,7 +28,7 @@ def check(sc: Scenario, partition_tokens: int = 0, brute: bool = True):
         rows = batch.token_index.cpu().tolist()
         exact = sc.brute_force(pool_ref)
         T = sc.q.shape[2]
-        got = out_gpu.view(-1, 12, 64).double().numpy()
+        got = out_gpu.view(-1, sc.H, 64).double().numpy()
         for r, flat in enumerate(rows):
             b, t = divmod(flat, T)
             np.testing.assert_allclose(got[r], exact[b][t], rtol=RTOL, atol=ATOL)
@@ -543,6 +543,30 @@ def test_prefill_two_query_tiles_per_wave_edges():
     starts = [rng.choice([0, 5, 16, 100]) for _ in lens]
     sc = Scenario(starts, lens, block_size=16, seed=77)
     check(sc, brute=False)
+
+
+@pytest.mark.parametrize("n_head", [1, 3, 16, 20, 25])
+@pytest.mark.parametrize("kind", ["decode", "prefill", "mixed"])
+def test_other_head_counts(n_head, kind):
+    """Head counts other than GPT-2 small's 12: GPT-2 medium / large / xl have 16 / 20 / 25 heads of
+    64, and 1 and 3 are small odd counts. The prefill grid deals (sequence, head) groups to the 8
+    XCDs, the decode split width depends on sequences x heads, and the mixed launch interleaves
+    both kinds of workgroup; each must match the reference path and float64 brute force."""
+    rng = random.Random(1000 + n_head)
+    if kind == "decode":
+        ctx = [rng.randint(1, 700) for _ in range(20)]
+        starts, lens = [c - 1 for c in ctx], [1] * len(ctx)
+    elif kind == "prefill":
+        starts, lens = [0, 37, 300, 16], [50, 17, 200, rng.randint(2, 40)]
+    else:
+        starts = [0, 130] + [rng.randint(0, 600) for _ in range(12)]
+        lens = [70, 33] + [1] * 12
+    sc = Scenario(starts, lens, block_size=16, seed=n_head, n_head=n_head)
+    _, batch = check(sc)
+    if kind == "mixed":
+        assert batch.num_decode > 0 and batch.num_prefill > 0
+    if kind == "decode":
+        check(sc, partition_tokens=64)  # the partition grid and its merge kernel
 
 
 @pytest.mark.parametrize("block_size", [8, 16])
