@@ -188,3 +188,54 @@ def test_chunked_prefill_with_preemption_matches_reference(gpu_model, ref_model)
     for seq, (_, prompt, n) in zip(seqs, specs):
         assert seq.output_token_ids == reference(ref_model, prompt, n)
     assert engine.allocator.num_free_blocks == 20
+
+
+@pytest.mark.parametrize("n_embd,n_head", [(1024, 16), (1600, 25)])
+def test_other_model_widths_match_reference(n_embd, n_head):
+    """Two-layer models at GPT-2 medium's and xl's widths (1024 / 16 heads, 1600 / 25 heads of 64),
+    4,000-token vocabulary: the engine (graphs, pipelining; the library GEMMs at every batch size,
+    since the fused small-batch linears take width 768 only) emits the oracle's greedy ids. A first
+    divergence is allowed only at a near tie (the oracle's top-1 / top-2 gap below 1e-4)."""
+    vocab, n_pos, n_new = 4000, 256, 24
+    cfg = GPT2Config(vocab_size=vocab, n_positions=n_pos, n_embd=n_embd, n_layer=2, n_head=n_head)
+    w = random_state_dict(cfg, seed=5)
+    m = GPT2(cfg)
+    m.load_state_dict(w)
+    m = m.cuda().eval()
+    ref = build_ref_model(RefConfig(vocab_size=vocab, n_positions=n_pos, n_embd=n_embd, n_layer=2, n_head=n_head), w)
+    rng = random.Random(n_head)
+    specs = sorted(((rng.randint(0, 6), [rng.randrange(vocab) for _ in range(rng.randint(5, 60))], n_new)
+                    for _ in range(6)), key=lambda spec: spec[0])  # run() returns sequences in arrival order
+    engine = Engine(m, BlockAllocator(cfg, 64, 16, device="cuda"))
+    seqs = run(engine, [(t, p, greedy(n)) for t, p, n in specs])
+    engine.allocator.check_device_errors()
+    for seq, (_, prompt, n) in zip(seqs, specs):
+        margins: list[float] = []
+        want = ref_greedy_generate(ref, list(prompt), n, margins)
+        got = seq.output_token_ids
+        assert len(got) == len(want) == n
+        k = next((i for i, (a, b) in enumerate(zip(got, want)) if a != b), None)
+        assert k is None or margins[k] < 1e-4, (k, margins[k] if k is not None else None)
+
+
+def test_zero_layer_model_matches_reference():
+    """A model without blocks (the reference's loop simply runs none): logits are ln_f of the
+    embeddings through the tied head."""
+    from tokquay_amd.generate import paged_forward
+    from tokquay_amd.sequence import Sequence
+
+    cfg = GPT2Config(vocab_size=4000, n_positions=256, n_layer=0)
+    w = random_state_dict(cfg, seed=6)
+    m = GPT2(cfg)
+    m.load_state_dict(w)
+    m = m.cuda().eval()
+    ref = build_ref_model(RefConfig(vocab_size=4000, n_positions=256, n_layer=0), w)
+    ids = text(40, 20)
+    ids = [t % 4000 for t in ids]
+    alloc = BlockAllocator(cfg, 8, 16, device="cuda")
+    seq = Sequence(0, ids)
+    alloc.allocate(seq)
+    got = paged_forward(m, alloc, [seq]).cpu()[0]
+    with torch.no_grad():
+        want = ref(torch.tensor([ids]))[0, -1]
+    torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-4)

@@ -94,7 +94,7 @@ class GPT2(nn.Module):
         sums ``wte[id] + wpe[pos]`` ``[N, C]`` if already computed (``ops.embed_rows``; ``ids`` and
         ``positions`` are then unused), updated in place as the residual stream."""
         blocks = self.h
-        first = blocks[0].ln_1
+        first = blocks[0].ln_1 if len(blocks) else self.ln_f  # no blocks: ln_f on the embeddings
         if embedded is None:
             x, h = ops.add_layernorm(self.wte(ids), self.wpe(positions), first.weight, first.bias, first.eps)
         else:
