@@ -545,6 +545,27 @@ def test_prefill_two_query_tiles_per_wave_edges():
     check(sc, brute=False)
 
 
+@pytest.mark.parametrize("block_size", [2, 3, 5, 64, 128, 1024])
+@pytest.mark.parametrize("kind", ["decode", "prefill", "mixed"])
+def test_unusual_block_sizes(block_size, kind):
+    """Block sizes the reference accepts beyond the usual powers of two up to 32: odd sizes (a
+    16-position chunk then spans blocks at uneven offsets) and large ones up to the 1024 maximum
+    (every sequence in one block); each must match the reference path and float64 brute force."""
+    rng = random.Random(2000 + block_size)
+    if kind == "decode":
+        ctx = [rng.randint(1, 600) for _ in range(12)] + [block_size, block_size + 1]
+        starts, lens = [c - 1 for c in ctx], [1] * len(ctx)
+    elif kind == "prefill":
+        starts, lens = [0, 37, block_size - 1, 5], [50, 17, 100, rng.randint(2, 40)]
+    else:
+        starts = [0, block_size + 3] + [rng.randint(0, 500) for _ in range(8)]
+        lens = [40, 21] + [1] * 8
+    sc = Scenario(starts, lens, block_size=block_size, seed=block_size)
+    check(sc)
+    if kind == "decode":
+        check(sc, partition_tokens=64)
+
+
 @pytest.mark.parametrize("n_head", [1, 3, 16, 20, 25])
 @pytest.mark.parametrize("kind", ["decode", "prefill", "mixed"])
 def test_other_head_counts(n_head, kind):
