@@ -239,3 +239,28 @@ def test_zero_layer_model_matches_reference():
     with torch.no_grad():
         want = ref(torch.tensor([ids]))[0, -1]
     torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-4)
+
+
+def test_sampled_generation_matches_reference_sampler(gpu_model, ref_model):
+    """Temperature / top-k rows (tokquay/engine.py:83-92): the engine's draws equal those of the
+    same sampler fed the oracle's fp32 logits, with the request's seed on a generator of the same
+    device. (Logits that differ by ~1e-6 pick differently only when a draw lands that close to a
+    boundary of the cumulative distribution.)"""
+    from tokquay_amd.engine import sample_token
+
+    specs = [(text(50 + i, 10 + 7 * i), SamplingParams(max_tokens=12, temperature=t, top_k=k, seed=100 + i,
+                                                         ignore_eos=True))
+             for i, (t, k) in enumerate([(0.8, 40), (1.0, 0), (0.5, 5), (1.3, 100)])]  # fmt: skip
+    engine = Engine(gpu_model, BlockAllocator(gpu_model.cfg, 64, 16, device="cuda"))
+    seqs = run(engine, [(0, p, sp) for p, sp in specs])
+    for seq, (prompt, sp) in zip(seqs, specs):
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(sp.seed)
+        ids, want = list(prompt), []
+        for _ in range(sp.max_tokens):
+            with torch.no_grad():
+                logits = ref_model(torch.tensor([ids]))[0, -1]
+            tok = sample_token(logits.cuda(), sp, gen)
+            want.append(tok)
+            ids.append(tok)
+        assert seq.output_token_ids == want
