@@ -242,15 +242,15 @@ def test_zero_layer_model_matches_reference():
 
 
 def test_sampled_generation_matches_reference_sampler(gpu_model, ref_model):
-    """Temperature / top-k rows (tokquay/engine.py:83-92): the engine's draws equal those of the
-    same sampler fed the oracle's fp32 logits, with the request's seed on a generator of the same
-    device. (Logits that differ by ~1e-6 pick differently only when a draw lands that close to a
-    boundary of the cumulative distribution.)"""
+    """Temperature / top-k rows (tokquay/engine.py:83-92), batched with greedy rows: the engine's
+    picks equal those of the same sampler fed the oracle's fp32 logits, with the request's seed on
+    a generator of the same device. (Logits that differ by ~1e-6 pick differently only when a draw
+    lands that close to a boundary of the cumulative distribution.)"""
     from tokquay_amd.engine import sample_token
 
     specs = [(text(50 + i, 10 + 7 * i), SamplingParams(max_tokens=12, temperature=t, top_k=k, seed=100 + i,
                                                          ignore_eos=True))
-             for i, (t, k) in enumerate([(0.8, 40), (1.0, 0), (0.5, 5), (1.3, 100)])]  # fmt: skip
+             for i, (t, k) in enumerate([(0.8, 40), (1.0, 0), (0.0, 0), (0.5, 5), (1.3, 100), (0.0, 0)])]  # fmt: skip
     engine = Engine(gpu_model, BlockAllocator(gpu_model.cfg, 64, 16, device="cuda"))
     seqs = run(engine, [(0, p, sp) for p, sp in specs])
     for seq, (prompt, sp) in zip(seqs, specs):
