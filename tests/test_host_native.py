@@ -130,6 +130,9 @@ def test_validation_order_and_messages(nat):
         PagedBatch(pool, 1024, [[0] * (2**21 + 1)], [2**31 - 1], [1])
     # The last context the kernels take is accepted.
     assert PagedBatch(pool, 1024, [[0] * 2**21], [2**31 - 2], [1]).max_ctx == 2**31 - 1
+    # Every context fits int32 but the batch's new tokens together do not (row offsets are int32).
+    with pytest.raises(ValueError, match="int32 rows"):
+        nat.plan([[0] * 16] * 3, [0, 0, 0], [2**30] * 3, 2**26)
     with pytest.raises(ValueError, match="do not match"):
         h = torch.empty(100, dtype=torch.int64)
         nat.fill([[0]], [0], [1], 4, h.data_ptr(), 3, h.data_ptr(), 50)

@@ -128,6 +128,11 @@ bool make_plan(PyObject* tables, PyObject* start, PyObject* new_lens, int64_t bs
       p->prefill_max_q = std::max(p->prefill_max_q, n);
     }
   }
+  // Row offsets (cu_seqlens) and row counts reach the kernels as int32.
+  if (p->N > (int64_t)INT32_MAX) {
+    PyErr_Format(PyExc_ValueError, "%lld new tokens in one batch exceed the kernels' int32 rows", (long long)p->N);
+    return false;
+  }
   return true;
 }
 
