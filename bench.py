@@ -820,7 +820,8 @@ def main() -> int:
         torch.cuda.synchronize()
         del engine, x, y
         torch.cuda.empty_cache()
-        _, mixed = mixed_chunked_step()  # config 5's chunk steps, as two launches and as one
+        # The 4-prompt chunked-prefill steps beside 128 decoding sequences, as two launches and as one.
+        _, mixed = mixed_chunked_step()
         print(json.dumps({"pmc_probe": True, "copy_bytes": 1 << 30,
                           "decode_bytes_first_step": decode_bytes(first_ctx),
                           "mixed_chunks": [{k: c[k] for k in ("chunk", "prefill_mflop", "decode_mb")} for c in mixed["chunks"]]}),

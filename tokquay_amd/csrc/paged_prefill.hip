@@ -251,7 +251,8 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
   // wave w loads float4 columns w, w + KS, ... of every lane's 16 dims here and the waves swap
   // them through LDS after issuing their first key tile's loads. At a launch's start every wave
   // otherwise asks for all of Q and two key tiles at once; sharing Q cuts that burst by 12 KB per
-  // 4-wave workgroup (config 5's chunk launches 11.7 / 20.0 / 27.1 -> 10.9 / 19.0 / 26.0 us).
+  // 4-wave workgroup (four 256-token prompt chunks at starts 0 / 256 / 512: 11.7 / 20.0 / 27.1 ->
+  // 10.9 / 19.0 / 26.0 us).
   constexpr bool kSharedQ = BS_CT == kTile && KS > 1 && KS <= 4;
   constexpr int kQShare = (4 + KS - 1) / KS;
   float4 qshare[kQShare];
