@@ -385,8 +385,12 @@ def test_gather_equals_the_reference_gather(block_size):
 
     err = torch.zeros(1, dtype=torch.int32, device="cuda")
     pool = sc.pool.cuda()
-    batch = PagedBatch(pool, block_size, sc.tables, sc.starts, sc.new_lens, error_word=err)
+    tables = [list(t) for t in sc.tables]
+    batch = PagedBatch(pool, block_size, tables, sc.starts, sc.new_lens, error_word=err)
     batch.write(sc.layer, sc.k.cuda(), sc.v.cuda())
+    for t in tables:  # the caller reuses its lists after the view is made: the view keeps its copy
+        t.reverse()
+        t.append(0)
     k, v = batch.gather(sc.layer)
     torch.cuda.synchronize()
     assert int(err.item()) == 0

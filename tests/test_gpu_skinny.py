@@ -158,6 +158,35 @@ def test_results_are_deterministic(N, K, M):
     torch.testing.assert_close(first.cpu(), F.linear(x.cpu(), w.cpu(), b.cpu()), **TOL)
 
 
+@pytest.mark.parametrize("M", [1, 8, 33, 64])
+def test_split_k_partials_are_never_stale(M):
+    """K = 3072 runs split over four workgroups per column block that hand their partial tiles to
+    the last one to arrive (relaxed agent-scope atomics, a wait and a barrier before the counter).
+    Three different inputs launched back to back 30 times, with no synchronisation between the
+    launches: a partial read before its writer's store is visible, or left over from the previous
+    launch, would change the bits. Each output equals its input's first output bit for bit, and
+    that one equals torch's fp32 product within tolerance, also with the residual epilogue."""
+    g = torch.Generator().manual_seed(100 + M)
+    xs = [torch.randn(M, 3072, generator=g).cuda() for _ in range(3)]
+    res = torch.randn(M, 768, generator=g).cuda()
+    w, b = (t.cuda() for t in weights(768, 3072, 9))
+    outs = [[], [], []]
+    for it in range(30):
+        for i, x in enumerate(xs):
+            if it % 2:
+                outs[i].append(ops.skinny_linear(x, w, b))
+            else:  # out += x @ w.T + b, into a fresh copy of the residual
+                outs[i].append(ops.skinny_linear(x, w, b, epilogue="residual", out=res.clone()))
+    torch.cuda.synchronize()
+    for i, x in enumerate(xs):
+        plain, resid = outs[i][1], outs[i][0]
+        for it, o in enumerate(outs[i]):
+            assert torch.equal(o, plain if it % 2 else resid), (i, it)
+        want = F.linear(x.cpu(), w.cpu(), b.cpu())
+        torch.testing.assert_close(plain.cpu(), want, **TOL)
+        torch.testing.assert_close(resid.cpu(), want + res.cpu(), **TOL)
+
+
 # ---- the LM head with the greedy argmax fused in (tq_skinny_linear_argmax) ----------------------
 def _lm_head_case(M: int, seed: int):
     g = torch.Generator().manual_seed(seed)

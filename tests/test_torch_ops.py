@@ -45,3 +45,42 @@ def test_a_traced_decode_layer_records_the_kernels_as_operators():
     targets = [str(n.target) for n in graph.graph.nodes if n.op == "call_function"]
     assert "tokquay_amd.paged_decode_write.default" in targets
     assert "tokquay_amd.argmax_rows.default" in targets
+
+
+# ---- argument checks: the fakes refuse what the operators refuse (tests/torch_op_cases.py)
+
+import pytest  # noqa: E402
+
+from tests.torch_op_cases import SIGS, base_args, cases, positional  # noqa: E402
+
+
+@pytest.mark.parametrize("op", list(SIGS))
+def test_fake_accepts_well_formed_arguments(op):
+    ops = torch_ops.load()
+    with FakeTensorMode():
+        getattr(ops, op)(*positional(op, base_args(op, "cuda")))
+
+
+@pytest.mark.parametrize("case", cases(), ids=lambda c: c.id)
+def test_fake_refuses_spoiled_arguments(case):
+    ops = torch_ops.load()
+    with FakeTensorMode():
+        args = base_args(case.op, "cuda")
+        args[case.arg] = case.spoil(args[case.arg])
+        with pytest.raises(RuntimeError, match=f"tokquay_amd::{case.op}: "):
+            getattr(ops, case.op)(*positional(case.op, args))
+
+
+def test_spoiled_cases_cover_every_tensor_argument():
+    spoiled = {(c.op, c.arg) for c in cases()}
+    for op, names in SIGS.items():
+        for a in names:
+            if a not in ("max_context_len", "max_query_len", "scale", "partition_tokens"):
+                assert (op, a) in spoiled, (op, a)
+
+
+def test_workspace_is_declared_written():
+    ops = torch_ops.load()
+    for op in ("paged_decode", "paged_decode_write", "paged_mixed"):
+        schema = str(getattr(ops, op).default._schema)
+        assert "!)? workspace" in schema, schema

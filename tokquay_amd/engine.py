@@ -16,10 +16,21 @@ The next step is launched ahead only when the synchronous engine would run the
 same decode step anyway: no request is waiting, every running sequence is in
 the batch, and the pool has room for every row's next slot without preempting.
 A row that will stop by length is left out; a row whose token turns out to be
-EOS is computed and discarded (its sequence is finished by then, so it emits
-nothing). Greedy ids per sequence are therefore those of the synchronous engine;
-the block ids a sequence receives may differ when a finishing sequence would
-have returned its blocks first.
+EOS (or whose request is aborted before the step is read) is computed and
+discarded: its sequence is finished by then, so it emits nothing. Greedy ids per
+sequence are therefore those of the synchronous engine; the block ids a sequence
+receives may differ when a finishing sequence would have returned its blocks
+first.
+
+Accounting follows the synchronous engine. A step launched ahead is settled at
+the start of the ``step()`` call that returns its tokens, once the previous
+step's finishes and any abort between the calls are applied: only then is it
+counted in ``stats`` and given its ``StepInfo``, over the rows whose sequences are
+still running (the rows the synchronous engine would have scheduled), with the
+KV snapshot of that moment. Its discarded rows go to ``positions_dropped``, so
+``positions_computed`` is the reference's count (needed + preemption-discarded
+positions); a step whose every row is discarded is dropped whole and the call
+schedules afresh, as the synchronous engine would.
 """
 
 from __future__ import annotations
@@ -59,6 +70,7 @@ class EngineStats:
     positions_padded: int = 0  # batch x longest row, the reference's padded work measure
     positions_discarded: int = 0  # cached positions thrown away by preemption
     lookahead_steps: int = 0  # decode steps launched before the previous step's tokens were read
+    positions_dropped: int = 0  # rows computed ahead, then discarded (their sequence had stopped)
 
 
 @dataclass
@@ -83,7 +95,7 @@ class _InFlight:
     seqs: list[Sequence]
     ids: torch.Tensor  # host int64 [n] the step's greedy ids are copied into
     ready: torch.cuda.Event | None  # recorded after that copy (None on the CPU)
-    info: StepInfo
+    info: StepInfo | None  # None until a step launched ahead is settled
 
 
 def finish_reason_for(seq: Sequence, token: int, eos_token_id: int) -> str | None:
@@ -155,7 +167,9 @@ class Engine:
         self._rngs.pop(seq.seq_id, None)
 
     def has_unfinished(self) -> bool:
-        return self._inflight is not None or self.scheduler.has_unfinished()
+        # A step in flight whose every row is discarded is not work left: step() drops it.
+        live = self._inflight is not None and any(s.status is SequenceStatus.RUNNING for s in self._inflight.seqs)
+        return live or self.scheduler.has_unfinished()
 
     def kv_snapshot(self) -> KVSnapshot:
         running = self.scheduler.running
@@ -168,6 +182,8 @@ class Engine:
     @torch.no_grad()
     def step(self) -> list[TokenEvent]:
         cur, self._inflight = self._inflight, None
+        if cur is not None and not self._settle(cur):
+            cur = None  # every row of the step launched ahead was discarded: schedule afresh
         if cur is None:
             batch = self.scheduler.schedule()
             if batch is None:
@@ -179,7 +195,12 @@ class Engine:
                 return self._run(batch)
             cur = self._launch(batch.seqs, None, batch.padded_tokens)
         self._inflight = self._lookahead(cur)
-        return self._complete(cur)
+        events = self._complete(cur)
+        nxt = self._inflight
+        if nxt is not None and not any(s.status is SequenceStatus.RUNNING for s in nxt.seqs):
+            self._settle(nxt)  # every row launched ahead stopped in `cur`: counted as dropped
+            self._inflight = None
+        return events
 
     def _count(self, seqs: list[Sequence], is_prefill: bool, fed: list[int], padded: int) -> None:
         st = self.stats
@@ -236,8 +257,9 @@ class Engine:
     def _can_pipeline(self, seqs: list[Sequence]) -> bool:
         return self.pipeline and self.graphs is not None and all(s.sampling.temperature == 0 for s in seqs)
 
-    def _launch(self, seqs: list[Sequence], src_rows: list[int] | None, padded: int) -> _InFlight:
-        """Enqueue one graph decode step and the copy of its greedy ids to the host."""
+    def _launch(self, seqs: list[Sequence], src_rows: list[int] | None, padded: int | None) -> _InFlight:
+        """Enqueue one graph decode step and the copy of its greedy ids to the host. ``padded`` is
+        None for a step launched ahead: its StepInfo is made when it is settled."""
         _, ids = self.graphs.launch(seqs, src_rows, logits=False)
         if self._host_ids is None:
             cap = self.graphs.capacity
@@ -249,7 +271,8 @@ class Engine:
         if ids.is_cuda:
             ready = torch.cuda.Event()
             ready.record()
-        return _InFlight(seqs, host, ready, StepInfo(False, len(seqs), padded, self.kv_snapshot()))
+        info = None if padded is None else StepInfo(False, len(seqs), padded, self.kv_snapshot())
+        return _InFlight(seqs, host, ready, info)
 
     def _lookahead(self, cur: _InFlight) -> _InFlight | None:
         """Launch the decode step after ``cur`` if the synchronous engine would run it unchanged."""
@@ -270,9 +293,22 @@ class Engine:
             return None  # the step may preempt: decided once the tokens are known
         for s in seqs:
             alloc.append_slot(s, s.num_cached_tokens + 1)
-        self._count(seqs, False, [1] * len(seqs), len(seqs))
         self.stats.lookahead_steps += 1
-        return self._launch(seqs, rows, len(seqs))
+        return self._launch(seqs, rows, None)
+
+    def _settle(self, cur: _InFlight) -> bool:
+        """Count a step launched ahead, now that the previous step's finishes are applied: its
+        rows of still-running sequences are the step the synchronous engine schedules here.
+        Returns False if no such row is left (the step is then dropped, uncounted)."""
+        if cur.info is not None:
+            return True
+        live = [s for s in cur.seqs if s.status is SequenceStatus.RUNNING]
+        self.stats.positions_dropped += len(cur.seqs) - len(live)
+        if not live:
+            return False
+        self._count(live, False, [1] * len(live), len(live))
+        cur.info = StepInfo(False, len(live), len(live), self.kv_snapshot())
+        return True
 
     def _complete(self, cur: _InFlight) -> list[TokenEvent]:
         if cur.ready is not None:
@@ -284,7 +320,9 @@ class Engine:
         """Read back the step launched ahead, if any, without launching another; afterwards every
         running sequence's tokens are on the host."""
         cur, self._inflight = self._inflight, None
-        return self._complete(cur) if cur is not None else []
+        if cur is None or not self._settle(cur):
+            return []
+        return self._complete(cur)
 
     def run_until_done(self) -> list[TokenEvent]:
         events = []

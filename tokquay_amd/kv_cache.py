@@ -217,8 +217,11 @@ class PagedBatch(BatchedKV):
         self.pool, self.block_size, self.B, self.T = pool, bs, B, T
         self.num_blocks_gathered = plan["max_blocks"]
         self.max_ctx = plan["max_ctx"]
-        self.start, self.new_lens = start, new_lens
-        self._tables = tables  # the callers' lists, for the reference view's gather
+        self.start, self.new_lens = list(start), list(new_lens)
+        # A copy of the tables as they are now (their first max_blocks entries), for the reference
+        # view's gather: a caller may grow, free or reuse its lists before gather() is called.
+        nb = plan["max_blocks"]
+        self._tables = [t[:nb] for t in tables]
         self.error_word = error_word
         self.partition_tokens = partition_tokens
         device = pool.device
@@ -354,7 +357,7 @@ class PagedBatch(BatchedKV):
 
         if "gather_tables" not in self._lazy:
             nb = self.num_blocks_gathered
-            padded = [list(t[:nb]) + [0] * (nb - len(t[:nb])) for t in self._tables]
+            padded = [list(t) + [0] * (nb - len(t)) for t in self._tables]
             self._lazy["gather_tables"] = torch.tensor(padded, dtype=torch.int32).to(self.device)
         return ops.paged_gather(self.pool, layer, self._lazy["gather_tables"], self.error_word)
 
