@@ -1,12 +1,16 @@
 """Decode throughput of the paged-attention engine on one MI355X.
 
 Workload (the decode-throughput configuration): GPT-2 124M, random-init fp32
-weights (normal std 0.02), 256 concurrent sequences whose context at the last
-decode step of the run is ~ U[256, 1024] (seeded), block size 16, KV pool of
-16,384 blocks (262,144 slots, 18 GiB). Prompts of random token ids are
-prefilled through the engine (untimed); then W warm-up and K timed decode steps
-run through ``Engine.step`` (scheduler + paged forward + sampling + the step's
-one sync).
+weights (normal std 0.02), 256 concurrent sequences, block size 16, KV pool of
+16,384 blocks (262,144 slots, 18 GiB). Each sequence draws a context c ~
+U[256 + K/2, 1024 - K/2] (seeded; K timed steps) and its prompt of random token
+ids is sized so that the K timed decode steps run at contexts c - K/2 ... c +
+K/2 - 1: the timed window is centred on the draw, its contexts lie in
+[256, 1024] and their mean is the draws' (~640). Prompts are prefilled through
+the engine (untimed); then W warm-up and K timed decode steps run through
+``Engine.step`` (scheduler + paged forward + sampling + the step's one sync).
+The decode kernel's own timing runs eagerly over the same K contexts, from the
+same state, before the timed steps (the engine's state is rewound in between).
 
 Prints one JSON line: decode tok/s (``value``), the decode-attention kernel's
 roofline (algorithmic bytes / live HIP-event kernel time vs 8 TB/s), and beside
@@ -139,7 +143,18 @@ def load_model(seed: int = 0):
     return model.cuda().eval()
 
 
-def build_engine(steps_needed: int, seed: int = 0):
+def window_draws(window: int, seed: int = 0) -> tuple[list[int], int, int]:
+    """Each sequence's context at the middle of a ``window``-step decode window, ~ U[lo, hi] with
+    lo = 256 + window // 2 and hi = 1024 - (window - 1 - window // 2): the window's contexts
+    c - window // 2 ... c + window - 1 - window // 2 then stay inside [256, 1024]."""
+    lo, hi = CTX_LO + window // 2, CTX_HI - (window - 1 - window // 2)
+    rng = random.Random(seed + 4)
+    return [rng.randint(lo, hi) for _ in range(N_SEQS)], lo, hi
+
+
+def build_engine(prompt_lens: list[int], max_tokens: int, seed: int = 0):
+    """The engine with one running sequence per prompt length (random token ids), prefilled
+    (untimed): each has its prompt cached and its first output token pending."""
     import torch
 
     from tokquay_amd.engine import Engine
@@ -150,17 +165,45 @@ def build_engine(steps_needed: int, seed: int = 0):
     model = load_model(seed)
     alloc = BlockAllocator(model.cfg, POOL_BLOCKS, BLOCK, device="cuda")
     engine = Engine(model, alloc, SchedulerConfig(max_num_seqs=N_SEQS, max_num_batched_tokens=32768, max_model_len=1024))
-    rng = random.Random(seed + 4)
-    final_ctx = [rng.randint(CTX_LO, CTX_HI) for _ in range(N_SEQS)]
-    for c in final_ctx:
-        prompt = [rng.randrange(50256) for _ in range(max(1, c - steps_needed))]
-        engine.add_request(prompt, SamplingParams(max_tokens=steps_needed + 2, ignore_eos=True))
+    rng = random.Random(seed + 5)
+    for n in prompt_lens:
+        prompt = [rng.randrange(50256) for _ in range(max(1, n))]
+        engine.add_request(prompt, SamplingParams(max_tokens=max_tokens, ignore_eos=True))
     t0 = time.perf_counter()
     while engine.scheduler.waiting:
-        engine.step()  # prefill steps (and a few decodes between them)
+        engine.step()  # prefill-only steps: admission comes first while the queue is not empty
     torch.cuda.synchronize()
     log(f"prefilled {N_SEQS} sequences in {time.perf_counter() - t0:.2f} s")
-    return engine, model, final_ctx
+    return engine, model
+
+
+def engine_state(engine) -> tuple:
+    """What decode steps change in the host state of an engine with nothing in flight and no
+    request waiting: the free list, the ref counts, the running list and each running sequence's
+    outputs, table, cached count and status. (The pool needs no copy: a step writes position p's
+    K/V before anything reads it, and a rewound run writes those slots again.)"""
+    alloc, sched = engine.allocator, engine.scheduler
+    assert engine._inflight is None and not sched.waiting
+    seqs = [(s, list(s.output_token_ids), list(s.block_table), s.num_cached_tokens, s.status, s.finish_reason)
+            for s in sched.running]  # fmt: skip
+    return list(alloc._free), list(alloc.ref_counts), list(sched.running), seqs
+
+
+def rewind(engine, state: tuple) -> None:
+    """Put a drained engine back in ``engine_state``'s state; sequences that finished by length
+    since are running again (no request may have arrived or been evicted in between)."""
+    engine.drain()
+    free, refs, running, seqs = state
+    sched = engine.scheduler
+    assert not sched.waiting and set(map(id, sched.running)) <= set(map(id, running))
+    engine.allocator._free[:] = free
+    engine.allocator.ref_counts[:] = refs
+    sched.running[:] = running
+    for s, out, table, cached, status, reason in seqs:
+        s.output_token_ids[:] = out
+        s.block_table[:] = table
+        s.num_cached_tokens = cached
+        s.status, s.finish_reason = status, reason
 
 
 def host_cpu_name() -> str:
@@ -800,13 +843,19 @@ def main() -> int:
             print(json.dumps(row), flush=True)
         return 0
 
-    # Warm-up, timed graph-replayed steps, eager kernel-timing steps, and the few steps the
-    # pipelined engine launches ahead or drains around them.
-    steps_needed = args.warmup + 2 * args.steps + 4
-    engine, model, drawn_ctx = build_engine(steps_needed)
+    # Step accounting, from the prefilled state (prompt P cached, one token pending). The W warm-up
+    # calls complete W steps and the drain one more: P + W + 1 cached (state S). From S the timed
+    # run completes one step untimed, whose call launches the next ahead; the K timed calls then
+    # hold the GPU work of the steps at contexts P + W + 4 ... P + W + K + 3. The prompt is sized so
+    # that this window is centred on the sequence's draw c: P = c - W - 4 - K // 2.
+    K, W = args.steps, args.warmup
+    drawn_ctx, draw_lo, draw_hi = window_draws(K)
+    # max_tokens: the run's last step emits each sequence's last token (prompt + max_tokens - 1
+    # = c + K - 1 - K // 2 <= 1024, the engine's limit).
+    engine, model = build_engine([c - W - 4 - K // 2 for c in drawn_ctx], max_tokens=W + K + 4)
     engine.allocator.decode_partition_tokens = args.partition_tokens
 
-    for _ in range(args.warmup):
+    for _ in range(W):
         engine.step()
     engine.drain()  # nothing in flight: every sequence's tokens are on the host
     if args.pmc_probe:
@@ -829,9 +878,10 @@ def main() -> int:
         return 0
     running = list(engine.scheduler.running)
     assert len(running) == N_SEQS, f"{len(running)} sequences running, expected {N_SEQS}"
-    # The state the next step starts from: the baselines start from it too.
+    # State S, the one the next step starts from: the baselines start from it too.
     state = [(list(s.block_table), s.num_cached_tokens, list(s.token_ids)) for s in running]
     order = {s.seq_id: i for i, s in enumerate(running)}
+    start = engine_state(engine)
 
     cpu_state = None
     if args.cpu_seqs > 0:
@@ -845,8 +895,28 @@ def main() -> int:
             ids[order[ev.seq_id]] = ev.token_id
         return ids
 
-    # The step after the snapshot. The engine launches the following step ahead, so the timed
-    # region starts in steady state.
+    # Kernel timing: the K decode steps of the timed window run eagerly from S (two untimed steps
+    # first, to reach the window), every decode launch timed by HIP events the launch itself
+    # records at the start and end of its kernels. Then the engine is rewound to S.
+    graphs, engine.graphs = engine.graphs, None
+    for _ in range(2):
+        engine.step()
+    eager_ctx = [s.num_cached_tokens + 1 for s in running]
+    timer = LaunchTimer("decode")
+    kv_cache.PagedBatch.launch_hook = timer
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(K):
+        engine.step()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t1) * 1e3 / K
+    kv_cache.PagedBatch.launch_hook = None
+    engine.graphs = graphs
+    engine.allocator.check_device_errors()
+    rewind(engine, start)
+
+    # The step after S. The engine launches the following step ahead, so the timed region starts
+    # in steady state.
     hip_steps = [by_row(engine.step())]
 
     # Timed region: K decode steps through Engine.step, replayed from the captured HIP graph.
@@ -855,7 +925,10 @@ def main() -> int:
     # Context of each row in the first step of GPU work inside the timed region (the step launched
     # ahead is already counted in num_cached_tokens).
     timed_ctx = [s.num_cached_tokens + 1 for s in running]
-    below = sorted({d - c for d, c in zip((drawn_ctx[s.seq_id] for s in running), timed_ctx)})
+    assert timed_ctx == eager_ctx, "the kernel-timing steps ran another window"
+    offsets = {c + K // 2 - d for d, c in zip((drawn_ctx[s.seq_id] for s in running), timed_ctx)}
+    assert offsets == {0}, f"timed window not centred on the draws: offsets {sorted(offsets)}"
+    assert max(timed_ctx) + K - 1 <= CTX_HI and min(timed_ctx) >= CTX_LO
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     emitted = []
@@ -870,20 +943,6 @@ def main() -> int:
     tok_s = n_tokens / elapsed
     mean_ctx_timed = statistics.mean(timed_ctx) + (args.steps - 1) / 2
     engine.drain()
-
-    # Kernel timing: K more decode steps run eagerly, every decode launch timed by HIP events
-    # the launch itself records at the start and end of its kernels.
-    graphs, engine.graphs = engine.graphs, None
-    timer = LaunchTimer("decode")
-    kv_cache.PagedBatch.launch_hook = timer
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    for _ in range(args.steps):
-        engine.step()
-    torch.cuda.synchronize()
-    eager_ms = (time.perf_counter() - t1) * 1e3 / args.steps
-    kv_cache.PagedBatch.launch_hook = None
-    engine.graphs = graphs
     engine.allocator.check_device_errors()
     n_launch = timer.launches("decode")
     kern_ms = timer.total_ms("decode") / n_launch
@@ -908,10 +967,10 @@ def main() -> int:
         "data": "synthetic: random-init weights (seed 0), random token ids",
         "config": {
             "workload": "scaled decode: GPT-2 124M fp32, 256 concurrent sequences, block_size 16, pool 16384 blocks "
-            "(262144 slots); contexts drawn U[256,1024] are each sequence's context after the run's last decode "
-            f"step, so the timed steps run {min(below) - args.steps + 1} to {max(below)} positions below the "
-            f"draws: mean context {mean_ctx_timed:.1f} over the timed steps (the draws' mean: "
-            f"{statistics.mean(drawn_ctx):.1f})",
+            f"(262144 slots); each sequence draws c ~ U[{draw_lo},{draw_hi}] and its {K} timed steps run at "
+            f"contexts c - {K // 2} ... c + {K - 1 - K // 2} (inside [256,1024]): mean context "
+            f"{mean_ctx_timed:.1f} over the timed steps (the draws' mean: {statistics.mean(drawn_ctx):.1f}); "
+            "the kernel-timing eager steps run the same contexts from the same state",
             "num_seqs": N_SEQS,
             "block_size": BLOCK,
             "pool_blocks": POOL_BLOCKS,
