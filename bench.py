@@ -942,6 +942,9 @@ def main() -> int:
     ms_per_step = elapsed * 1e3 / args.steps
     tok_s = n_tokens / elapsed
     mean_ctx_timed = statistics.mean(timed_ctx) + (args.steps - 1) / 2
+    # The blocks every position of the window went to (read before the drain: the drained step
+    # emits each sequence's last token, and finishing frees its table).
+    tables_after = [list(s.block_table) for s in running]
     engine.drain()
     engine.allocator.check_device_errors()
     n_launch = timer.launches("decode")
@@ -998,7 +1001,6 @@ def main() -> int:
     weights = random_state_dict(model.cfg, seed=0)
     if args.gather_steps > 0:
         log(f"GPU gather baseline: {N_SEQS} sequences, {args.gather_steps} timed steps ...")
-        tables_after = [list(s.block_table) for s in running]
         gb = baseline_gpu_gather(engine.allocator.pool, state, tables_after, hip_steps, weights, args.gather_steps)
         gb["speedup_of_hip_engine"] = round(tok_s / gb["value"], 2)
         result["gpu_gather_baseline"] = gb
