@@ -144,12 +144,18 @@ def load_model(seed: int = 0):
 
 
 def window_draws(window: int, seed: int = 0) -> tuple[list[int], int, int]:
-    """Each sequence's context at the middle of a ``window``-step decode window, ~ U[lo, hi] with
-    lo = 256 + window // 2 and hi = 1024 - (window - 1 - window // 2): the window's contexts
-    c - window // 2 ... c + window - 1 - window // 2 then stay inside [256, 1024]."""
+    """Each sequence's context at the middle of a ``window``-step decode window, uniform on [lo, hi]
+    with lo = 256 + window // 2 and hi = 1024 - (window - 1 - window // 2): the window's contexts
+    c - window // 2 ... c + window - 1 - window // 2 then stay inside [256, 1024]. Stratified: the
+    i-th of the 256 draws is uniform on the i-th 1/256 of the range, and the draws are shuffled, so
+    each is still uniform on [lo, hi] while their mean is the range's to within a position
+    (256 independent draws put it anywhere within about +-27 of it, at two standard deviations)."""
     lo, hi = CTX_LO + window // 2, CTX_HI - (window - 1 - window // 2)
     rng = random.Random(seed + 4)
-    return [rng.randint(lo, hi) for _ in range(N_SEQS)], lo, hi
+    width = (hi - lo + 1) / N_SEQS
+    draws = [lo + int((i + rng.random()) * width) for i in range(N_SEQS)]
+    rng.shuffle(draws)
+    return draws, lo, hi
 
 
 def build_engine(prompt_lens: list[int], max_tokens: int, seed: int = 0):
@@ -970,7 +976,8 @@ def main() -> int:
         "data": "synthetic: random-init weights (seed 0), random token ids",
         "config": {
             "workload": "scaled decode: GPT-2 124M fp32, 256 concurrent sequences, block_size 16, pool 16384 blocks "
-            f"(262144 slots); each sequence draws c ~ U[{draw_lo},{draw_hi}] and its {K} timed steps run at "
+            f"(262144 slots); each sequence draws c ~ U[{draw_lo},{draw_hi}] (stratified over the 256) and its {K} "
+            "timed steps run at "
             f"contexts c - {K // 2} ... c + {K - 1 - K // 2} (inside [256,1024]): mean context "
             f"{mean_ctx_timed:.1f} over the timed steps (the draws' mean: {statistics.mean(drawn_ctx):.1f}); "
             "the kernel-timing eager steps run the same contexts from the same state",
