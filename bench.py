@@ -31,12 +31,15 @@ them:
 
 Other modes (each prints one JSON line and exits): ``--small-batch N`` (decode
 step p50 at N sequences), ``--configs`` (the small configurations side by side
-with the gather path), ``--pmc-probe`` (a short run for counter collection).
+with the gather path), ``--prefill-op`` (the prefill kernel alone on synthetic
+shapes, also part of the main line as ``prefill_op_alone``), ``--pmc-probe`` (a
+short run for counter collection).
 """
 
 from __future__ import annotations
 
 import argparse
+import itertools
 import json
 import math
 import os
@@ -355,6 +358,100 @@ def prefill_batch(seed: int = 32, reps: int = 3) -> dict:
             "bound": "mfma", "us_per_launch": round(us, 2), "mflop_per_launch": round(flops / 1e6, 1),
             "achieved": round(flops / us / 1e6, 2), "peak": MFMA_FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(flops / us / 1e6 / MFMA_FP32_PEAK_TFLOPS, 4)}  # fmt: skip
+
+
+def hbm_copy(reps: int = 20) -> dict:
+    """A reference for the HBM bandwidth this box sustains: torch's device-to-device copy of 1 GiB
+    (1 GiB read + 1 GiB written), each copy bracketed by events; median."""
+    import torch
+
+    x = torch.randn(1 << 28, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    pairs = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        y.copy_(x)
+        b.record()
+        pairs.append((a, b))
+    torch.cuda.synchronize()
+    us = statistics.median(a.elapsed_time(b) for a, b in pairs) * 1e3
+    moved = 2 << 30
+    return {"workload": "torch copy_ of 1 GiB on the device (1 GiB read + 1 GiB written), median of 20",
+            "us": round(us, 1), "GBs": round(moved / us / 1e3, 1), "frac": round(moved / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
+def prefill_op_alone(reps: int = 25) -> dict:
+    """The prefill kernel alone (``tq_paged_prefill`` on a one-layer pool with seeded random K/V, q
+    and block tables dealt from a random permutation of the pool), each shape launched ``reps`` times
+    back to back, every launch timed by the events it records; median per shape. Shapes: config 5's
+    four chunks alone (``mixed_chunked_step``'s 4 prompts in 256-token chunks), 32 prompts U[256,1024]
+    at start 0 (seed 32), and long prompts (2 x 8192, 16 x 2048 at start 0), whose key loops are
+    long enough that launch start and end amortise: the kernel's steady state."""
+    import torch
+
+    from tokquay_amd import _lib, ops
+
+    lib = _lib.lib()
+
+    def shapes():
+        rng = random.Random(5)  # mixed_chunked_step's draws: each prompt's length, then its token ids
+        plen = []
+        for _ in range(4):
+            plen.append(rng.randint(512, 1024))
+            for _ in range(plen[-1]):
+                rng.randrange(50256)
+        for k in range(4):
+            starts = [256 * k for p in plen if p > 256 * k]
+            yield f"config 5 chunk {k}", starts, [min(256, p - 256 * k) for p in plen if p > 256 * k]
+        rng = random.Random(32)
+        yield "32 prompts U[256,1024]", [0] * 32, [rng.randint(256, 1024) for _ in range(32)]
+        yield "2 prompts x 8192", [0, 0], [8192, 8192]
+        yield "16 prompts x 2048", [0] * 16, [2048] * 16
+
+    out = []
+    g = torch.Generator(device="cuda").manual_seed(11)
+    for name, starts, lens in shapes():
+        nblk = [cdiv(s + n, BLOCK) for s, n in zip(starts, lens)]
+        nb = sum(nblk) + 8
+        pool = torch.randn(nb, 1, 2, N_HEAD, BLOCK, D_HEAD, device="cuda", generator=g)
+        perm = torch.randperm(nb, generator=torch.Generator().manual_seed(12)).tolist()
+        tables = torch.zeros(len(lens), max(nblk), dtype=torch.int32)
+        i = 0
+        for r, n in enumerate(nblk):
+            tables[r, :n] = torch.tensor(perm[i : i + n], dtype=torch.int32)
+            i += n
+        rows = sum(lens)
+        q = torch.randn(rows, N_HEAD * D_HEAD, device="cuda", generator=g)
+        o = torch.empty_like(q)
+        cu = torch.tensor([0] + list(itertools.accumulate(lens)), dtype=torch.int32, device="cuda")
+        st = torch.tensor(starts, dtype=torch.int32, device="cuda")
+        tables = tables.cuda()
+        err = torch.zeros(1, dtype=torch.int32, device="cuda")
+        call = lambda: ops.paged_prefill(o, q, pool, 0, tables, cu, st, max(lens), d_error=err)  # noqa: E731
+        for _ in range(3):
+            call()
+        torch.cuda.synchronize()
+        pairs = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            b.record()
+            lib.tq_set_timing_events(a.cuda_event, b.cuda_event)
+            call()
+            pairs.append((a, b))
+        torch.cuda.synchronize()
+        assert int(err.item()) == 0
+        us = statistics.median(a.elapsed_time(b) for a, b in pairs) * 1e3
+        flops = prefill_flops(starts, lens)
+        out.append({"shape": name, "rows": rows, "mflop": round(flops / 1e6, 1), "us": round(us, 2),
+                    "tflops": round(flops / us / 1e6, 2), "frac": round(flops / us / 1e6 / MFMA_FP32_PEAK_TFLOPS, 4)})
+        del pool, q, o
+    return {"workload": "tq_paged_prefill alone on a one-layer pool (random K/V, q, permuted tables), "
+                        f"launched {reps} times back to back per shape; median launch", "shapes": out}
 
 
 def mixed_chunked_step(seed: int = 5) -> tuple[dict, dict]:
@@ -825,6 +922,8 @@ def main() -> int:
     ap.add_argument("--small-batch", type=int, default=0, metavar="N",
                     help="only measure decode-step wall time at N sequences (300-token prompts) and exit")
     ap.add_argument("--small-batch-steps", type=int, default=80, help="tokens per sequence for --small-batch")
+    ap.add_argument("--prefill-op", action="store_true",
+                    help="only time the prefill kernel alone (chunks, a 32-prompt batch, long prompts) and exit")
     ap.add_argument("--configs", action="store_true",
                     help="only run the small configurations beside the gather path (GPU and CPU) and exit")
     ap.add_argument("--pmc-probe", action="store_true",
@@ -843,6 +942,9 @@ def main() -> int:
     torch.manual_seed(0)
     if args.small_batch:
         print(json.dumps(small_batch(args.small_batch, args.small_batch_steps)), flush=True)
+        return 0
+    if args.prefill_op:
+        print(json.dumps(prefill_op_alone()), flush=True)
         return 0
     if args.configs:
         for row in baseline_configs():
@@ -1033,6 +1135,7 @@ def main() -> int:
     torch.cuda.empty_cache()
     log("decode op alone (64 sequences, ctx U[16,512]) ...")
     result["decode_op_alone"] = decode_op_alone()
+    result["hbm_copy"] = hbm_copy()
     if not args.no_prefill:
         log("mixed chunked-prefill + decode steps ...")
         result["prefill"], result["mixed_attention"] = mixed_chunked_step()
@@ -1043,6 +1146,8 @@ def main() -> int:
         result["prefill_batch"] = prefill_batch()
         log(f"prefill batch: {result['prefill_batch']['us_per_launch']} us per launch = "
             f"{result['prefill_batch']['frac']:.3f} of fp32 MFMA peak")
+        log("prefill kernel alone (chunks, a 32-prompt batch, long prompts) ...")
+        result["prefill_op_alone"] = prefill_op_alone()
         result["mixed_engine"] = [mixed_engine(chunked=True), mixed_engine(chunked=False)]
         torch.cuda.empty_cache()
     if not args.no_itl:
