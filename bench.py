@@ -388,8 +388,8 @@ def prefill_op_alone(reps: int = 25) -> dict:
     """The prefill kernel alone (``tq_paged_prefill`` on a one-layer pool with seeded random K/V, q
     and block tables dealt from a random permutation of the pool), each shape launched ``reps`` times
     back to back, every launch timed by the events it records; median per shape. Shapes: config 5's
-    four chunks alone (``mixed_chunked_step``'s 4 prompts in 256-token chunks), 32 prompts U[256,1024]
-    at start 0 (seed 32), and long prompts (2 x 8192, 16 x 2048 at start 0), whose key loops are
+    four chunks alone (``mixed_chunked_step``'s 4 prompts in 256-token chunks), ``prefill_batch``'s 32
+    prompts U[256,1024] at start 0, and long prompts (2 x 8192, 16 x 2048 at start 0), whose key loops are
     long enough that launch start and end amortise: the kernel's steady state."""
     import torch
 
@@ -407,8 +407,13 @@ def prefill_op_alone(reps: int = 25) -> dict:
         for k in range(4):
             starts = [256 * k for p in plen if p > 256 * k]
             yield f"config 5 chunk {k}", starts, [min(256, p - 256 * k) for p in plen if p > 256 * k]
-        rng = random.Random(32)
-        yield "32 prompts U[256,1024]", [0] * 32, [rng.randint(256, 1024) for _ in range(32)]
+        rng = random.Random(32)  # prefill_batch's draws: each prompt's length, then its token ids
+        lens = []
+        for _ in range(32):
+            lens.append(rng.randint(256, 1024))
+            for _ in range(lens[-1]):
+                rng.randrange(50256)
+        yield "32 prompts U[256,1024] (prefill_batch's prompts)", [0] * 32, lens
         yield "2 prompts x 8192", [0, 0], [8192, 8192]
         yield "16 prompts x 2048", [0] * 16, [2048] * 16
 
@@ -431,7 +436,11 @@ def prefill_op_alone(reps: int = 25) -> dict:
         st = torch.tensor(starts, dtype=torch.int32, device="cuda")
         tables = tables.cuda()
         err = torch.zeros(1, dtype=torch.int32, device="cuda")
-        call = lambda: ops.paged_prefill(o, q, pool, 0, tables, cu, st, max(lens), d_error=err)  # noqa: E731
+        # The batch view's dispatch order: most causal work first (stable).
+        work = [n * (2 * s + n + 1) for s, n in zip(starts, lens)]
+        order = torch.tensor(sorted(range(len(lens)), key=lambda b: -work[b]), dtype=torch.int32, device="cuda")
+        call = lambda: ops.paged_prefill(o, q, pool, 0, tables, cu, st, max(lens), d_error=err,  # noqa: E731
+                                         seq_order=order)
         for _ in range(3):
             call()
         torch.cuda.synchronize()
@@ -450,8 +459,9 @@ def prefill_op_alone(reps: int = 25) -> dict:
         out.append({"shape": name, "rows": rows, "mflop": round(flops / 1e6, 1), "us": round(us, 2),
                     "tflops": round(flops / us / 1e6, 2), "frac": round(flops / us / 1e6 / MFMA_FP32_PEAK_TFLOPS, 4)})
         del pool, q, o
-    return {"workload": "tq_paged_prefill alone on a one-layer pool (random K/V, q, permuted tables), "
-                        f"launched {reps} times back to back per shape; median launch", "shapes": out}
+    return {"workload": "tq_paged_prefill alone on a one-layer pool (random K/V, q, permuted tables, the batch "
+                        f"view's most-work-first sequence order), launched {reps} times back to back per shape; "
+                        "median launch", "shapes": out}
 
 
 def mixed_chunked_step(seed: int = 5) -> tuple[dict, dict]:

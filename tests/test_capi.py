@@ -47,7 +47,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_status_strings_and_version(lib):
-    assert lib.tq_abi_version() == 2
+    assert lib.tq_abi_version() == 3
     assert lib.tq_status_string(0) == b"ok"
     assert lib.tq_status_string(3) == b"workspace missing or too small"
     assert lib.tq_last_hip_error() == b""
@@ -78,8 +78,11 @@ def test_invalid_arguments_are_rejected_before_any_launch(lib):
     assert lib.tq_paged_decode_write(None, 768, None, 2304, None, 2304, None, 2304, None, 8, 1, 12, 16, 64, 0,
                                      None, 4, 4, None, None, 0, 64, 0.125, 0, None, 0, None, None) == 0  # fmt: skip
     # prefill: zero sequences is a no-op
-    assert lib.tq_paged_prefill(None, 768, None, 768, None, 8, 1, 12, 16, 64, 0, None, 4, 4, None, None,
+    assert lib.tq_paged_prefill(None, 768, None, 768, None, 8, 1, 12, 16, 64, 0, None, 4, 4, None, None, None,
                                 0, 0, 0, 0.125, None, None) == 0  # fmt: skip
+    # prefill: null pointers with rows to do
+    assert lib.tq_paged_prefill(None, 768, None, 768, None, 8, 1, 12, 16, 64, 0, None, 4, 4, None, None, None,
+                                2, 32, 16, 0.125, None, None) == 1  # fmt: skip
 
 
 def test_decode_workspace_size(lib):

@@ -549,6 +549,57 @@ def test_prefill_two_query_tiles_per_wave_edges():
     check(sc, brute=False)
 
 
+@pytest.mark.parametrize("num_seqs,max_len", [(80, 400), (40, 300), (4, 256)])
+def test_prefill_dispatch_order_does_not_change_results(num_seqs, max_len):
+    """seq_order only changes how a launch deals its sequences: identical bits for no order, the
+    most-work-first order the batch view passes and a random permutation. One-wave launches (two
+    query tiles per wave at 80 sequences, one at 40) report an entry out of range (TQ_DEVERR_ORDER)
+    and skip that sequence; a key-split launch (4 sequences) ignores the order."""
+    from tokquay_amd import _lib, ops
+
+    rng = random.Random(num_seqs)
+    lens = [rng.randint(16, max_len) for _ in range(num_seqs)]
+    starts = [rng.choice([0, 0, 7, 100]) for _ in range(num_seqs)]
+    ctx = [s + n for s, n in zip(starts, lens)]
+    nb = sum(cdiv(c, 16) for c in ctx) + 4
+    pool = torch.randn(nb, 1, 2, 12, 16, 64, generator=torch.Generator().manual_seed(num_seqs)).cuda()
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(num_seqs + 1)).tolist()
+    width = max(cdiv(c, 16) for c in ctx)
+    tables = torch.zeros(num_seqs, width, dtype=torch.int32)
+    i = 0
+    for b, c in enumerate(ctx):
+        tables[b, : cdiv(c, 16)] = torch.tensor(perm[i : i + cdiv(c, 16)], dtype=torch.int32)
+        i += cdiv(c, 16)
+    tables = tables.cuda()
+    cu_l = [0]
+    for n in lens:
+        cu_l.append(cu_l[-1] + n)
+    cu = torch.tensor(cu_l, dtype=torch.int32, device="cuda")
+    st = torch.tensor(starts, dtype=torch.int32, device="cuda")
+    q = torch.randn(cu_l[-1], 768, generator=torch.Generator().manual_seed(num_seqs + 2)).cuda()
+    work = [n * (2 * s + n + 1) for s, n in zip(starts, lens)]
+    outs = []
+    for order in (None, sorted(range(num_seqs), key=lambda b: -work[b]), torch.randperm(num_seqs).tolist()):
+        out = torch.empty_like(q)
+        so = None if order is None else torch.tensor(order, dtype=torch.int32, device="cuda")
+        ops.paged_prefill(out, q, pool, 0, tables, cu, st, max(lens), seq_order=so)
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    bad = torch.arange(num_seqs, dtype=torch.int32, device="cuda")
+    bad[2] = num_seqs + 5
+    out = torch.zeros_like(q)
+    ops.paged_prefill(out, q, pool, 0, tables, cu, st, max(lens), d_error=err, seq_order=bad)
+    torch.cuda.synchronize()
+    rows_of_2 = list(range(cu_l[2], cu_l[3]))
+    keep = [r for r in range(cu_l[-1]) if r not in set(rows_of_2)]
+    assert torch.equal(out[keep], outs[0][keep])
+    if num_seqs > 4:
+        assert int(err.item()) == _lib.DEVERR_ORDER
+    else:
+        assert int(err.item()) == 0 and torch.equal(out, outs[0])
+
+
 @pytest.mark.parametrize("block_size", [2, 3, 5, 64, 128, 1024])
 @pytest.mark.parametrize("kind", ["decode", "prefill", "mixed"])
 def test_unusual_block_sizes(block_size, kind):

@@ -51,7 +51,7 @@ class HipRefPagedBatch(RefPagedBatch):
         nb = self.tables32.size(1)
         _lib.check(L_.tq_paged_prefill(out.data_ptr(), C, q.data_ptr(), C, self.pool.data_ptr(), NB, L, H, bs, d,
                                        layer, self.tables32.data_ptr(), nb, nb, self.cu.data_ptr(),
-                                       self.start_t.data_ptr(), B, N, self.max_q, 1 / math.sqrt(d), None,
+                                       self.start_t.data_ptr(), None, B, N, self.max_q, 1 / math.sqrt(d), None,
                                        self.stream), "prefill")  # fmt: skip
         full = out.new_zeros(B * T, C)
         full[self.idx] = out

@@ -61,8 +61,11 @@ def expected(tables, starts, lens, bs):
     dctx = [starts[b] + 1 for b in dec]
     cu = np.cumsum([0] + [lens[b] for b in pre]).tolist()
     order = sorted(range(len(dec)), key=lambda i: (-dctx[i], i))  # longest first, stable
+    # Multi-token sequences by causal work (sum over the rows of the keys each sees), most first, stable.
+    work = [sum(starts[b] + t + 1 for t in range(lens[b])) for b in pre]
+    pre_order = sorted(range(len(pre)), key=lambda i: (-work[i], i))
     i64 = tok + pos + slot + last
-    i32 = dt.ravel().tolist() + dctx + pt.ravel().tolist() + cu + [starts[b] for b in pre] + order
+    i32 = dt.ravel().tolist() + dctx + pt.ravel().tolist() + cu + [starts[b] for b in pre] + order + pre_order
     return i64, i32
 
 
@@ -139,7 +142,7 @@ def test_validation_order_and_messages(nat):
 
 
 def test_attend_entry_rejects_bad_sizes_without_launching(nat):
-    args = [0] * 30
+    args = [0] * 31
     args[9] = 0.125
     args[12] = 0  # N = 0
     with pytest.raises(ValueError):

@@ -22,7 +22,7 @@ SIGS = {
     "paged_decode_write": ["out", "q", "k_new", "v_new", "pool", "layer", "block_tables", "context_lens",
                            "max_context_len", "scale", "partition_tokens", "workspace", "d_error", "seq_order"],
     "paged_prefill": ["out", "q", "pool", "layer", "block_tables", "cu_seqlens_q", "q_start", "max_query_len", "scale",
-                      "d_error"],
+                      "d_error", "seq_order"],
     "paged_mixed": ["dec_out", "dec_q", "k_new", "v_new", "dec_block_tables", "context_lens", "max_context_len",
                     "pre_out", "pre_q", "pre_block_tables", "cu_seqlens_q", "q_start", "max_query_len", "pool", "layer",
                     "scale", "partition_tokens", "workspace", "d_error", "seq_order"],
@@ -64,7 +64,7 @@ def base_args(op: str, device, workspace_bytes: Callable[[str], int] = lambda op
     elif op == "paged_decode_write":
         a = dict(common, **dec, **ws, out=f(3, W), q=f(3, H, D), k_new=f(3, W), v_new=f(3, H, D))
     elif op == "paged_prefill":
-        a = dict(common, **pre, out=f(7, W), q=f(7, H, D))
+        a = dict(common, **pre, out=f(7, W), q=f(7, H, D), seq_order=i32([1, 0]))
     elif op == "paged_mixed":
         a = dict(common, **ws, dec_out=f(3, W), dec_q=f(3, H, D), k_new=f(3, W), v_new=f(3, W),
                  dec_block_tables=dec["block_tables"], context_lens=dec["context_lens"],

@@ -107,7 +107,7 @@ SIGNATURES: dict[str, tuple] = {
             c_f32p, ctypes.c_int64, ctypes.c_int32,  # pool, num_blocks, num_layers
             ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,  # num_heads, block_size, head_dim, layer
             c_i32p, ctypes.c_int64, ctypes.c_int32,  # block_tables, block_table_stride, max_blocks_per_seq
-            c_i32p, c_i32p,  # cu_seqlens_q, q_start
+            c_i32p, c_i32p, c_i32p,  # cu_seqlens_q, q_start, seq_order
             ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,  # num_seqs, num_q_rows, max_query_len
             ctypes.c_float, c_i32p, ctypes.c_void_p,  # scale, d_error, stream
         ],

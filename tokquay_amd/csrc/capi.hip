@@ -42,6 +42,6 @@ extern "C" const char* tq_status_string(tq_status status) {
   return "unknown status";
 }
 
-extern "C" int32_t tq_abi_version(void) { return 2; }
+extern "C" int32_t tq_abi_version(void) { return 3; }
 
 extern "C" const char* tq_last_hip_error(void) { return g_last_hip_error; }

@@ -17,10 +17,11 @@
 // sequences feeding several tokens, contiguous per sequence. Metadata layout:
 //   int64: token_index[N] | positions[N] | slot_mapping[N] | last_rows[B]
 //   int32: dec_tables[Bd][nbd] | dec_ctx[Bd] | pre_tables[Bp][nbp] | pre_cu[Bp + 1]
-//          | pre_start[Bp] | dec_order[Bd]
+//          | pre_start[Bp] | dec_order[Bd] | pre_order[Bp]
 // token_index[r] = b * T + t for row r holding token t of sequence b (T = longest new
 // run); dec_order lists the decode rows by decreasing context (stable), the decode
-// kernel's dispatch order.
+// kernel's dispatch order; pre_order the multi-token sequences by decreasing causal work
+// n * (start + n / 2) (stable), the prefill kernel's.
 
 #define PY_SSIZE_T_CLEAN
 #include <Python.h>
@@ -137,7 +138,7 @@ bool make_plan(PyObject* tables, PyObject* start, PyObject* new_lens, int64_t bs
 }
 
 int64_t n64_of(const Plan& p) { return 3 * p.N + p.B; }
-int64_t n32_of(const Plan& p) { return p.Bd * p.nbd + p.Bd + p.Bp * p.nbp + (p.Bp + 1) + p.Bp + p.Bd; }
+int64_t n32_of(const Plan& p) { return p.Bd * p.nbd + p.Bd + p.Bp * p.nbp + (p.Bp + 1) + p.Bp + p.Bd + p.Bp; }
 
 PyObject* py_plan(PyObject*, PyObject* args) {
   PyObject *tables, *start, *new_lens;
@@ -177,6 +178,7 @@ PyObject* py_fill(PyObject*, PyObject* args) {
   int32_t* pre_cu = pre_tables + Bp * nbp;
   int32_t* pre_start = pre_cu + Bp + 1;
   int32_t* dec_order = pre_start + Bp;
+  int32_t* pre_order = dec_order + Bd;
   int64_t di = 0, pi = 0, row = Bd;
   for (Py_ssize_t b = 0; b < (Py_ssize_t)B; ++b) {
     int64_t s = 0, n = 0;
@@ -222,26 +224,33 @@ PyObject* py_fill(PyObject*, PyObject* args) {
   pre_cu[Bp] = (int32_t)(N - Bd);
   std::iota(dec_order, dec_order + Bd, 0);
   std::stable_sort(dec_order, dec_order + Bd, [&](int32_t x, int32_t y) { return dec_ctx[x] > dec_ctx[y]; });
+  // Twice the causal work of sequence i: each of its n rows sees start + its index + 1 keys.
+  auto work2 = [&](int32_t i) {
+    const int64_t n = (int64_t)pre_cu[i + 1] - pre_cu[i];
+    return n * (2 * (int64_t)pre_start[i] + n + 1);
+  };
+  std::iota(pre_order, pre_order + Bp, 0);
+  std::stable_sort(pre_order, pre_order + Bp, [&](int32_t x, int32_t y) { return work2(x) > work2(y); });
   Py_RETURN_NONE;
 }
 
 // attend(out, qkv, pool, num_blocks, num_layers, num_heads, block_size, head_dim, layer, scale, stream,
 //        error_word, N, Bd, dec_tables, nbd, dec_ctx, dec_order, decode_max_ctx, partition_tokens,
-//        workspace, workspace_bytes, Bp, slot_mapping, pre_tables, nbp, pre_cu, pre_start, prefill_max_q,
-//        mixed)
+//        workspace, workspace_bytes, Bp, slot_mapping, pre_tables, nbp, pre_cu, pre_start, pre_order,
+//        prefill_max_q, mixed)
 // launches one layer's kernels for a packed batch (device pointers and the stream as Python ints).
 // Returns None, or (status, entry point name) for the first launch that failed.
 PyObject* py_attend(PyObject*, PyObject* args) {
   unsigned long long out, qkv, pool, stream, d_error, dec_tables, dec_ctx, dec_order, workspace, slot_mapping,
-      pre_tables, pre_cu, pre_start;
+      pre_tables, pre_cu, pre_start, pre_order;
   long long num_blocks, N, Bd, nbd, decode_max_ctx, ws_bytes, Bp, nbp, prefill_max_q;
   int num_layers, num_heads, block_size, head_dim, layer, partition_tokens, mixed;
   float scale;
-  if (!PyArg_ParseTuple(args, "KKKLiiiiifKKLLKLKKLiKLLKKLKKLp", &out, &qkv, &pool, &num_blocks, &num_layers,
+  if (!PyArg_ParseTuple(args, "KKKLiiiiifKKLLKLKKLiKLLKKLKKKLp", &out, &qkv, &pool, &num_blocks, &num_layers,
                         &num_heads, &block_size, &head_dim, &layer, &scale, &stream, &d_error, &N, &Bd,
                         &dec_tables, &nbd, &dec_ctx, &dec_order, &decode_max_ctx, &partition_tokens, &workspace,
-                        &ws_bytes, &Bp, &slot_mapping, &pre_tables, &nbp, &pre_cu, &pre_start, &prefill_max_q,
-                        &mixed))
+                        &ws_bytes, &Bp, &slot_mapping, &pre_tables, &nbp, &pre_cu, &pre_start, &pre_order,
+                        &prefill_max_q, &mixed))
     return nullptr;
   if (N < 1 || Bd < 0 || Bp < 0 || nbd < 0 || nbp < 0 || ws_bytes < 0) {
     PyErr_SetString(PyExc_ValueError, "attend: negative sizes");
@@ -292,7 +301,8 @@ PyObject* py_attend(PyObject*, PyObject* args) {
         s = tq_paged_prefill(o + Bd * C, C, qp, row3, pl, num_blocks, num_layers, num_heads, block_size, head_dim,
                              layer, reinterpret_cast<const int32_t*>(pre_tables), nbp, (int32_t)nbp,
                              reinterpret_cast<const int32_t*>(pre_cu), reinterpret_cast<const int32_t*>(pre_start),
-                             (int32_t)Bp, (int32_t)(N - Bd), (int32_t)prefill_max_q, scale, err, st);
+                             reinterpret_cast<const int32_t*>(pre_order), (int32_t)Bp, (int32_t)(N - Bd),
+                             (int32_t)prefill_max_q, scale, err, st);
         if (s != TQ_OK) what = "tq_paged_prefill";
       }
     }

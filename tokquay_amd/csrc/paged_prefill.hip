@@ -64,6 +64,7 @@ struct PrefillArgs {
   int64_t bt_stride;
   const int32_t* cu_q;
   const int32_t* q_start;
+  const int32_t* seq_order;  // dispatch rank -> sequence, or nullptr for the natural order
   int32_t* d_error;
   float scale;
   int32_t num_blocks;
@@ -95,7 +96,8 @@ constexpr int kRound = 64;    // dispatches per XCD taken as one round (two per 
 // about as well, 16 worse; dealing contiguous runs of groups instead of every
 // eighth group left a 3-prompt chunk with one long prompt 45 % slower). Returns
 // false for a padding workgroup. `p` is the workgroup's index among the launch's prefill
-// workgroups, a multiple of 8 dispatches after the first (so p % 8 is still its XCD).
+// workgroups, a multiple of 8 dispatches after the first (so p % 8 is still its XCD). The
+// sequence b it returns is a dispatch rank; a.seq_order maps it to the sequence itself.
 __device__ __forceinline__ bool tile_of(const PrefillArgs& a, int p, int& qt, int& h, int& b) {
   const int xcd = p % kXcds, local = p / kXcds;
   const int G = (a.groups - xcd + kXcds - 1) / kXcds;  // groups xcd, xcd + 8, ... on this XCD
@@ -207,8 +209,12 @@ __device__ __forceinline__ void load_kv_block_tile(const PrefillArgs& a, const f
 // The work of prefill workgroup `dispatch` (its KS waves): QH consecutive query tiles of one head
 // of one sequence, or nothing for a padding workgroup. QH = 2 (one wave per workgroup only) feeds
 // each key tile's loads to twice the MFMAs and gives the wave two independent softmax chains.
-template <int BS_CT, int KS, int QH = 1>
+// PIPE: the software-pipelined key loop (block size 16 only). The mixed launch keeps the plain
+// loop for its 8-wave workgroups: the pipelined one needs 138 VGPRs there, which leaves a CU
+// room for one such workgroup instead of two, and its decode workgroups share the kernel.
+template <int BS_CT, int KS, int QH = 1, bool PIPE = (BS_CT == kTile)>
 __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int dispatch) {
+  static_assert(!PIPE || BS_CT == kTile, "the pipelined key loop reads one block per key tile");
   static_assert(QH == 1 || KS == 1, "two query tiles per wave only without a key split");
   const int lane = threadIdx.x & (kWave - 1);
   // Wave-uniform by construction; readfirstlane lets the compiler keep the key-tile loop
@@ -216,6 +222,14 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   int qt, h, b;
   if (!tile_of(a, dispatch, qt, h, b)) return;  // padding workgroup (uniform)
+  if (a.seq_order != nullptr) {
+    const int sb = a.seq_order[b];
+    if ((uint32_t)sb >= (uint32_t)a.num_seqs) {
+      if (qt == 0 && h == 0 && threadIdx.x == 0) flag_error(a.d_error, TQ_DEVERR_ORDER);
+      return;
+    }
+    b = sb;
+  }
   const int bs = BS_CT > 0 ? BS_CT : a.block_size;
 
   const int row0 = a.cu_q[b];
@@ -247,13 +261,13 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
   // B operand of the QK product: Q[query j][16g + s], s = 0..15, pre-scaled by
   // scale * log2(e) so the scores come out in log2 units for v_exp_f32.
   const float qscale = a.scale * kLog2e;
-  // The pipelined key split (block size 16, 2 or 4 waves) reads the tile's Q once per workgroup:
+  // The pipelined key split (block size 16, 2 to 8 waves) reads the tile's Q once per workgroup:
   // wave w loads float4 columns w, w + KS, ... of every lane's 16 dims here and the waves swap
   // them through LDS after issuing their first key tile's loads. At a launch's start every wave
   // otherwise asks for all of Q and two key tiles at once; sharing Q cuts that burst by 12 KB per
   // 4-wave workgroup (four 256-token prompt chunks at starts 0 / 256 / 512: 11.7 / 20.0 / 27.1 ->
   // 10.9 / 19.0 / 26.0 us).
-  constexpr bool kSharedQ = BS_CT == kTile && KS > 1 && KS <= 4;
+  constexpr bool kSharedQ = PIPE && KS > 1;
   constexpr int kQShare = (4 + KS - 1) / KS;
   float4 qshare[kQShare];
   float qreg[QH][16];
@@ -364,8 +378,8 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
       }
   };
 
-  if constexpr (BS_CT == kTile && KS <= 4) {
-    // Block size 16 and at most 4 waves per workgroup: tile i is block table entry i.
+  if constexpr (PIPE) {
+    // Block size 16: tile i is block table entry i.
     // The ids of 64 consecutive tiles are held one per lane and fetched per tile with
     // v_readlane (no table loads in the loop); the lane copy is refreshed when the
     // wave moves to the next 64.
@@ -571,11 +585,12 @@ void launch_prefill_ks(const PrefillArgs& a, hipStream_t stream, hipEvent_t star
 
 // Waves per workgroup: the largest key split KS that still lets every workgroup of
 // the launch be resident at once (a second round of workgroups costs more than the
-// split saves). The pipelined kernel (KS <= 4) holds 3 waves per SIMD, so a CU
-// takes 12 / KS of its workgroups: KS = 4 up to 768 tiles, 2 up to 1536. The KS = 8
-// instance runs the plain loop, one workgroup per CU: up to 256 tiles. Measured on
-// 256-token chunks: 768 tiles run best with 4, 960 with 2, 576 with 4; KS = 16 on
-// 192-252 tiles ran 15-20 % slower than 8.
+// split saves). The pipelined kernel holds 3 waves per SIMD, so a CU takes 12 / KS of
+// its workgroups: KS = 4 up to 768 tiles, 2 up to 1536. The KS = 8 instance takes one
+// workgroup per CU (its LDS reservation): up to 256 tiles. Measured on 256-token chunks:
+// 768 tiles run best with 4, 960 with 2, 576 with 4; KS = 16 (plain loop) on 192-252
+// tiles ran 15-20 % slower than 8; the pipelined loop at KS = 8 took a 3-prompt tail
+// chunk with 5 / 102 / 9 rows at position 768 from 15.1 to 13.8 us.
 int choose_key_split(int64_t tiles) {
   constexpr int kCus = 256;
   constexpr int kSlotsPipelined = 12;  // wave slots per CU at 3 waves per SIMD
@@ -591,9 +606,16 @@ int choose_key_split(int64_t tiles) {
 // prompts 3.5 % faster.)
 constexpr int64_t kTwoTileMinTiles = 8192;
 
+// The sequence order applies to one-wave launches only: there, dealing the sequences' tiles
+// longest first (each XCD's share of the heavy sequences, then the rounds' mix) ran 3-16 %
+// faster on six draws of 32 prompts U[256,1024]. Key-split launches hold every workgroup at
+// once and keep the natural order.
 template <int BS_CT>
-void launch_prefill(const PrefillArgs& a, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
-  switch (choose_key_split((int64_t)a.groups * a.qtiles)) {
+void launch_prefill(const PrefillArgs& a_in, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+  const int ks = choose_key_split((int64_t)a_in.groups * a_in.qtiles);
+  PrefillArgs a = a_in;
+  if (ks != 1) a.seq_order = nullptr;
+  switch (ks) {
     case 1:
       if (BS_CT == kTile && (int64_t)a.num_heads * ((a.num_q_rows + kTile - 1) / kTile) >= kTwoTileMinTiles) {
         // More tiles than the key split pays for, and many rows: with block size 16 each wave
@@ -629,6 +651,7 @@ struct PrefillCall {
   int32_t max_blocks_per_seq;
   const int32_t* cu_seqlens_q;
   const int32_t* q_start;
+  const int32_t* seq_order;
   int32_t num_seqs, num_q_rows, max_query_len;
   float scale;
   int32_t* d_error;
@@ -670,6 +693,7 @@ tq_status make_prefill_args(const PrefillCall& c, PrefillArgs& a, bool& empty) {
   a.bt_stride = c.block_table_stride;
   a.cu_q = c.cu_seqlens_q;
   a.q_start = c.q_start;
+  a.seq_order = c.seq_order;
   a.d_error = c.d_error;
   a.scale = c.scale;
   a.num_blocks = (int32_t)c.num_blocks;
@@ -739,7 +763,7 @@ __global__ __launch_bounds__(kWave* KS) void mixed_kernel(const PrefillArgs p, c
     decode_unit<DEC_BS, true>(d, rest / d.max_parts, u - rest * d.num_heads, rest % d.max_parts, lane);
     return;
   }
-  prefill_workgroup<PRE_BS, KS>(p, idx);
+  prefill_workgroup<PRE_BS, KS, 1, PRE_BS == kTile && KS <= 4>(p, idx);
 }
 
 template <int DEC_BS, int PRE_BS, int KS>
@@ -773,16 +797,16 @@ extern "C" tq_status tq_paged_prefill(float* out, int64_t out_row_stride, const 
                                       int32_t head_dim, int32_t layer, const int32_t* block_tables,
                                       int64_t block_table_stride, int32_t max_blocks_per_seq,
                                       const int32_t* cu_seqlens_q, const int32_t* q_start,
-                                      int32_t num_seqs, int32_t num_q_rows, int32_t max_query_len,
-                                      float scale, int32_t* d_error, void* stream) {
+                                      const int32_t* seq_order, int32_t num_seqs, int32_t num_q_rows,
+                                      int32_t max_query_len, float scale, int32_t* d_error, void* stream) {
   using namespace tq;
   const TimingEvents timing = take_timing_events();  // for this call only, whatever it returns
   PrefillArgs a;
   bool empty;
   const tq_status st = make_prefill_args({out, out_row_stride, q, q_row_stride, pool, num_blocks, num_layers,
                                           num_heads, block_size, head_dim, layer, block_tables, block_table_stride,
-                                          max_blocks_per_seq, cu_seqlens_q, q_start, num_seqs, num_q_rows,
-                                          max_query_len, scale, d_error},
+                                          max_blocks_per_seq, cu_seqlens_q, q_start, seq_order, num_seqs,
+                                          num_q_rows, max_query_len, scale, d_error},
                                          a, empty);
   if (st != TQ_OK || empty) return st;
   hipStream_t s = (hipStream_t)stream;
@@ -835,8 +859,8 @@ extern "C" tq_status tq_paged_mixed(float* dec_out, int64_t dec_out_row_stride, 
   if (num_decode_seqs == 0)
     return tq_paged_prefill(pre_out, pre_out_row_stride, pre_q, pre_q_row_stride, pool, num_blocks, num_layers,
                             num_heads, block_size, head_dim, layer, pre_block_tables, pre_block_table_stride,
-                            pre_max_blocks_per_seq, cu_seqlens_q, q_start, num_prefill_seqs, num_q_rows,
-                            max_query_len, scale, d_error, stream);
+                            pre_max_blocks_per_seq, cu_seqlens_q, q_start, nullptr, num_prefill_seqs,
+                            num_q_rows, max_query_len, scale, d_error, stream);
 
   const TimingEvents timing = take_timing_events();  // for this call only, whatever it returns
   if (k_new == nullptr || v_new == nullptr || pool == nullptr) return TQ_ERR_INVALID_ARGUMENT;
@@ -845,7 +869,7 @@ extern "C" tq_status tq_paged_mixed(float* dec_out, int64_t dec_out_row_stride, 
   tq_status st = make_prefill_args({pre_out, pre_out_row_stride, pre_q, pre_q_row_stride, pool, num_blocks,
                                     num_layers, num_heads, block_size, head_dim, layer, pre_block_tables,
                                     pre_block_table_stride, pre_max_blocks_per_seq, cu_seqlens_q, q_start,
-                                    num_prefill_seqs, num_q_rows, max_query_len, scale, d_error},
+                                    nullptr, num_prefill_seqs, num_q_rows, max_query_len, scale, d_error},
                                    pa, empty);
   if (st != TQ_OK) return st;
   const int ks = choose_key_split((int64_t)pa.groups * pa.qtiles);

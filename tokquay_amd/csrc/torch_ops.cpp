@@ -197,17 +197,20 @@ int64_t prefill_args(const char* op, const Pool& p, const at::Tensor& out, const
 
 void paged_prefill(at::Tensor out, const at::Tensor& q, const at::Tensor& pool, int64_t layer,
                    const at::Tensor& block_tables, const at::Tensor& cu_seqlens_q, const at::Tensor& q_start,
-                   int64_t max_query_len, double scale, const c10::optional<at::Tensor>& d_error) {
+                   int64_t max_query_len, double scale, const c10::optional<at::Tensor>& d_error,
+                   const c10::optional<at::Tensor>& seq_order) {
   const char* op = "tokquay_amd::paged_prefill";
   const Pool p = pool_of(op, pool, layer);
   const int64_t n = prefill_args(op, p, out, q, "out", "q", "block_tables", block_tables, cu_seqlens_q, q_start);
+  if (seq_order.has_value()) vector_of(op, "seq_order", *seq_order, at::kInt, n, p);
   error_word_of(op, d_error, p);
   const int64_t nq = q.size(0);
   check(tq_paged_prefill(out.data_ptr<float>(), rows_of(op, "out", out, nq, p), q.data_ptr<float>(),
                          rows_of(op, "q", q, nq, p), pool.data_ptr<float>(), p.blocks, p.layers, p.heads,
                          p.block_size, p.head_dim, (int32_t)layer, block_tables.data_ptr<int32_t>(),
                          tables_of(op, "block_tables", block_tables, n, p), (int32_t)block_tables.size(1),
-                         cu_seqlens_q.data_ptr<int32_t>(), q_start.data_ptr<int32_t>(), (int32_t)n, (int32_t)nq,
+                         cu_seqlens_q.data_ptr<int32_t>(), q_start.data_ptr<int32_t>(), ptr<int32_t>(seq_order),
+                         (int32_t)n, (int32_t)nq,
                          (int32_t)max_query_len, (float)scale, ptr<int32_t>(d_error), stream_of(pool)),
         "tq_paged_prefill");
 }
@@ -289,7 +292,7 @@ TORCH_LIBRARY(tokquay_amd, m) {
         "Tensor block_tables, Tensor context_lens, int max_context_len, float scale, int partition_tokens, "
         "Tensor(c!)? workspace, Tensor(d!)? d_error, Tensor? seq_order) -> ()");
   m.def("paged_prefill(Tensor(a!) out, Tensor q, Tensor pool, int layer, Tensor block_tables, Tensor cu_seqlens_q, "
-        "Tensor q_start, int max_query_len, float scale, Tensor(b!)? d_error) -> ()");
+        "Tensor q_start, int max_query_len, float scale, Tensor(b!)? d_error, Tensor? seq_order) -> ()");
   m.def("paged_mixed(Tensor(a!) dec_out, Tensor dec_q, Tensor k_new, Tensor v_new, Tensor dec_block_tables, "
         "Tensor context_lens, int max_context_len, Tensor(b!) pre_out, Tensor pre_q, Tensor pre_block_tables, "
         "Tensor cu_seqlens_q, Tensor q_start, int max_query_len, Tensor(c!) pool, int layer, float scale, "

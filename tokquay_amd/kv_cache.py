@@ -235,6 +235,7 @@ class PagedBatch(BatchedKV):
         # int64: token_index[N] | positions[N] | slot_mapping[N] | last_rows[B]
         # int32: dec_tables[Bd, nbd] | dec_ctx[Bd] | pre_tables[Bp, nbp] | pre_cu[Bp + 1] | pre_start[Bp]
         #        | dec_order[Bd] (decode rows, longest context first: the decode kernel's dispatch order)
+        #        | pre_order[Bp] (multi-token sequences, most causal work first: the prefill kernel's)
         h64 = torch.empty(plan["n64"], dtype=torch.int64, pin_memory=pin)
         h32 = torch.empty(plan["n32"], dtype=torch.int32, pin_memory=pin)
         nat.fill(tables, start, new_lens, bs, h64.data_ptr(), h64.numel(), h32.data_ptr(), h32.numel())
@@ -242,7 +243,7 @@ class PagedBatch(BatchedKV):
         self._d32 = h32.to(device, non_blocking=True)
         # Element offsets of the int32 sections; the views below are made on first use.
         self._o32 = (0, Bd * nbd, Bd * nbd + Bd, Bd * nbd + Bd + Bp * nbp, Bd * nbd + Bd + Bp * nbp + Bp + 1,
-                     Bd * nbd + Bd + Bp * nbp + 2 * Bp + 1)  # fmt: skip
+                     Bd * nbd + Bd + Bp * nbp + 2 * Bp + 1, Bd * nbd + 2 * Bd + Bp * nbp + 2 * Bp + 1)  # fmt: skip
         self._workspace: torch.Tensor | None = None
         self._ws_bytes = 0
         self._ws_mixed = False  # the workspace was sized for the one-launch mixed grid
@@ -257,7 +258,8 @@ class PagedBatch(BatchedKV):
         return t
 
     def _ptr32(self, i: int) -> int:
-        """Device address of int32 section ``i`` (dec_tables, dec_ctx, pre_tables, pre_cu, pre_start, dec_order)."""
+        """Device address of int32 section ``i`` (dec_tables, dec_ctx, pre_tables, pre_cu, pre_start, dec_order,
+        pre_order)."""
         return self._d32.data_ptr() + 4 * self._o32[i]
 
     @property
@@ -301,6 +303,10 @@ class PagedBatch(BatchedKV):
     @property
     def decode_order(self) -> torch.Tensor:
         return self._view("decode_order", self._d32, self._o32[5], self._o32[5] + self.num_decode)
+
+    @property
+    def prefill_order(self) -> torch.Tensor:
+        return self._view("prefill_order", self._d32, self._o32[6], self._o32[6] + self.num_prefill)
 
     # ---- reference contract members (built on demand; the HIP path does not need them) ----
     @property
@@ -411,7 +417,8 @@ class PagedBatch(BatchedKV):
                 op, qp, pp, nb, n_layer, n_head, bs, d, layer, scale, stream, err or 0, N,
                 Bd, self._ptr32(0), self._nbd, self._ptr32(1), self._ptr32(5), self.decode_max_ctx,
                 self.partition_tokens, ws, self._ws_bytes,
-                Bp, slots, self._ptr32(2), self._nbp, self._ptr32(3), self._ptr32(4), self.prefill_max_q, int(mixed),
+                Bp, slots, self._ptr32(2), self._nbp, self._ptr32(3), self._ptr32(4), self._ptr32(6), self.prefill_max_q,
+                int(mixed),
             )  # fmt: skip
             if failed is not None:
                 _lib.check(*failed)
@@ -449,8 +456,8 @@ class PagedBatch(BatchedKV):
             PagedBatch.launch_hook(self, "prefill")
             _lib.check(
                 L.tq_paged_prefill(op + 4 * Bd * C, C, qp + off, row3, pp, nb, n_layer, n_head, bs, d, layer,
-                                   self._ptr32(2), self._nbp, self._nbp, self._ptr32(3), self._ptr32(4), Bp, N - Bd,
-                                   self.prefill_max_q, scale, err, stream),
+                                   self._ptr32(2), self._nbp, self._nbp, self._ptr32(3), self._ptr32(4),
+                                   self._ptr32(6), Bp, N - Bd, self.prefill_max_q, scale, err, stream),
                 "tq_paged_prefill",
             )  # fmt: skip
         return out

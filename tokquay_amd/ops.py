@@ -162,9 +162,12 @@ def paged_prefill(
     max_query_len: int,
     scale: float | None = None,
     d_error: torch.Tensor | None = None,
+    seq_order: torch.Tensor | None = None,
 ) -> None:
     """Causal attention of each sequence's new rows ``cu_seqlens_q[b]:cu_seqlens_q[b+1]`` (positions
-    ``q_start[b]...``) over its keys ``0 .. q_start[b] + n_b - 1`` read in place from the pool."""
+    ``q_start[b]...``) over its keys ``0 .. q_start[b] + n_b - 1`` read in place from the pool.
+    ``seq_order`` (int32 ``[B]``, a permutation): the order large launches deal the sequences in;
+    most causal work first is fastest."""
     nb, n_layer, n_head, bs, d = _pool_dims(pool)
     if not 0 <= layer < n_layer:
         raise ValueError(f"layer {layer} out of range [0, {n_layer})")
@@ -181,7 +184,12 @@ def paged_prefill(
     _rows(q, "q", n_rows, n_head, pool.device)
     _rows(out, "out", n_rows, n_head, pool.device)
     scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
-    _op("paged_prefill", out, q, pool, layer, block_tables, cu_seqlens_q, q_start, int(max_query_len), scale, d_error)
+    if seq_order is not None:
+        _int_tensor(seq_order, "seq_order", torch.int32, pool.device)
+        if seq_order.numel() != n_seq:
+            raise ValueError(f"seq_order needs {n_seq} entries")
+    _op("paged_prefill", out, q, pool, layer, block_tables, cu_seqlens_q, q_start, int(max_query_len), scale, d_error,
+        seq_order)  # fmt: skip
 
 
 def _tables(t: torch.Tensor, name: str, n: int, device: torch.device) -> int:

@@ -13,7 +13,7 @@ or entries, overlapping rows:
   partition_tokens, workspace!?, d_error!?, seq_order?)``
 * ``paged_decode_write(out!, q, k_new, v_new, pool!, layer, ...)`` (the same, with the cache write)
 * ``paged_prefill(out!, q, pool, layer, block_tables, cu_seqlens_q, q_start, max_query_len, scale,
-  d_error!?)``
+  d_error!?, seq_order?)``
 * ``paged_mixed(dec_out!, dec_q, k_new, v_new, dec_block_tables, context_lens, max_context_len,
   pre_out!, pre_q, pre_block_tables, cu_seqlens_q, q_start, max_query_len, pool!, layer, scale,
   partition_tokens, workspace!?, d_error!?, seq_order?)``
@@ -162,10 +162,13 @@ def _prefill_args(op, pool, out, q, out_name, q_name, tables_name, block_tables,
     _tables_of(op, tables_name, block_tables, n, pool)
 
 
-def _fake_paged_prefill(out, q, pool, layer, block_tables, cu_seqlens_q, q_start, max_query_len, scale, d_error):
+def _fake_paged_prefill(out, q, pool, layer, block_tables, cu_seqlens_q, q_start, max_query_len, scale, d_error,
+                        seq_order):  # fmt: skip
     op = "paged_prefill"
     _pool_of(op, pool, layer)
     _prefill_args(op, pool, out, q, "out", "q", "block_tables", block_tables, cu_seqlens_q, q_start)
+    if seq_order is not None:
+        _vector_of(op, "seq_order", seq_order, torch.int32, q_start.numel(), pool)
     _error_word(op, d_error, pool)
 
 
