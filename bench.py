@@ -389,8 +389,9 @@ def prefill_op_alone(reps: int = 25) -> dict:
     and block tables dealt from a random permutation of the pool), each shape launched ``reps`` times
     back to back, every launch timed by the events it records; median per shape. Shapes: config 5's
     four chunks alone (``mixed_chunked_step``'s 4 prompts in 256-token chunks), ``prefill_batch``'s 32
-    prompts U[256,1024] at start 0, and long prompts (2 x 8192, 16 x 2048 at start 0), whose key loops are
-    long enough that launch start and end amortise: the kernel's steady state."""
+    prompts U[256,1024] at start 0, long prompts (2 x 8192, 16 x 2048 at start 0), whose key loops are
+    long enough that launch start and end amortise: the kernel's steady state, and one prompt of one row
+    (12 workgroups of one key tile): the span of a launch with almost nothing to do."""
     import torch
 
     from tokquay_amd import _lib, ops
@@ -415,6 +416,7 @@ def prefill_op_alone(reps: int = 25) -> dict:
                 rng.randrange(50256)
         yield "32 prompts U[256,1024] (prefill_batch's prompts)", [0] * 32, lens
         yield "2 prompts x 8192", [0, 0], [8192, 8192]
+        yield "1 prompt x 1 row (launch span)", [0], [1]
         yield "16 prompts x 2048", [0] * 16, [2048] * 16
 
     out = []
