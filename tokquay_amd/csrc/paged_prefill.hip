@@ -210,8 +210,8 @@ __device__ __forceinline__ void load_kv_block_tile(const PrefillArgs& a, const f
 // of one sequence, or nothing for a padding workgroup. QH = 2 (one wave per workgroup only) feeds
 // each key tile's loads to twice the MFMAs and gives the wave two independent softmax chains.
 // PIPE: the software-pipelined key loop (block size 16 only). The mixed launch keeps the plain
-// loop for its 8-wave workgroups: the pipelined one needs 138 VGPRs there, which leaves a CU
-// room for one such workgroup instead of two, and its decode workgroups share the kernel.
+// loop: its decode workgroups share the kernel, and the pipelined loop's 130-138 VGPRs would hold
+// them to 3 waves per SIMD instead of 4 (config 5's chunk steps ran about 1 % slower with it).
 template <int BS_CT, int KS, int QH = 1, bool PIPE = (BS_CT == kTile)>
 __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int dispatch) {
   static_assert(!PIPE || BS_CT == kTile, "the pipelined key loop reads one block per key tile");
@@ -763,7 +763,7 @@ __global__ __launch_bounds__(kWave* KS) void mixed_kernel(const PrefillArgs p, c
     decode_unit<DEC_BS, true>(d, rest / d.max_parts, u - rest * d.num_heads, rest % d.max_parts, lane);
     return;
   }
-  prefill_workgroup<PRE_BS, KS, 1, PRE_BS == kTile && KS <= 4>(p, idx);
+  prefill_workgroup<PRE_BS, KS, 1, false>(p, idx);
 }
 
 template <int DEC_BS, int PRE_BS, int KS>
