@@ -422,6 +422,9 @@ def prefill_op_alone(reps: int = 25) -> dict:
     out = []
     g = torch.Generator(device="cuda").manual_seed(11)
     for name, starts, lens in shapes():
+        # The 32-prompt shape also runs in the natural sequence order, on the same inputs, its
+        # launches alternating with the ordered ones.
+        compare = name.startswith("32 prompts")
         nblk = [cdiv(s + n, BLOCK) for s, n in zip(starts, lens)]
         nb = sum(nblk) + 8
         pool = torch.randn(nb, 1, 2, N_HEAD, BLOCK, D_HEAD, device="cuda", generator=g)
@@ -441,29 +444,32 @@ def prefill_op_alone(reps: int = 25) -> dict:
         # The batch view's dispatch order: most causal work first (stable).
         work = [n * (2 * s + n + 1) for s, n in zip(starts, lens)]
         order = torch.tensor(sorted(range(len(lens)), key=lambda b: -work[b]), dtype=torch.int32, device="cuda")
-        call = lambda: ops.paged_prefill(o, q, pool, 0, tables, cu, st, max(lens), d_error=err,  # noqa: E731
-                                         seq_order=order)
+        variants = [(name, order)] + ([(name + ", natural order", None)] if compare else [])
         for _ in range(3):
-            call()
+            for _, so in variants:
+                ops.paged_prefill(o, q, pool, 0, tables, cu, st, max(lens), d_error=err, seq_order=so)
         torch.cuda.synchronize()
-        pairs = []
+        pairs = [[] for _ in variants]
         for _ in range(reps):
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            b.record()
-            lib.tq_set_timing_events(a.cuda_event, b.cuda_event)
-            call()
-            pairs.append((a, b))
+            for i, (_, so) in enumerate(variants):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                b.record()
+                lib.tq_set_timing_events(a.cuda_event, b.cuda_event)
+                ops.paged_prefill(o, q, pool, 0, tables, cu, st, max(lens), d_error=err, seq_order=so)
+                pairs[i].append((a, b))
         torch.cuda.synchronize()
         assert int(err.item()) == 0
-        us = statistics.median(a.elapsed_time(b) for a, b in pairs) * 1e3
         flops = prefill_flops(starts, lens)
-        out.append({"shape": name, "rows": rows, "mflop": round(flops / 1e6, 1), "us": round(us, 2),
-                    "tflops": round(flops / us / 1e6, 2), "frac": round(flops / us / 1e6 / MFMA_FP32_PEAK_TFLOPS, 4)})
+        for (vname, _), ps in zip(variants, pairs):
+            us = statistics.median(a.elapsed_time(b) for a, b in ps) * 1e3
+            out.append({"shape": vname, "rows": rows, "mflop": round(flops / 1e6, 1), "us": round(us, 2),
+                        "tflops": round(flops / us / 1e6, 2),
+                        "frac": round(flops / us / 1e6 / MFMA_FP32_PEAK_TFLOPS, 4)})  # fmt: skip
         del pool, q, o
     return {"workload": "tq_paged_prefill alone on a one-layer pool (random K/V, q, permuted tables, the batch "
-                        f"view's most-work-first sequence order), launched {reps} times back to back per shape; "
-                        "median launch", "shapes": out}
+                        f"view's most-work-first sequence order unless named), launched {reps} times back to back per "
+                        "shape; median launch", "shapes": out}
 
 
 def mixed_chunked_step(seed: int = 5) -> tuple[dict, dict]:
