@@ -527,7 +527,7 @@ def test_launch_recorded_timing_events():
 def test_prefill_key_split_widths(block_size, num_seqs):
     """The prefill launch splits each query tile's keys over 1, 2, 4 or 8 waves depending on how many
     tiles there are (4608 / 1536 / 768 / 192 query tiles -> 1 / 2 / 4 / 8 waves), for the
-    block-size-16 path (one block per key tile; software-pipelined up to 4 waves; the one-wave
+    block-size-16 path (one block per key tile; software-pipelined at every width; the one-wave
     launch takes two query tiles per wave) and the generic one; every width must match the
     reference, with ragged lengths and chunk starts."""
     rng = random.Random(num_seqs)
