@@ -27,7 +27,8 @@
 // accumulators are rescaled, only when a score passes it by more than 2^8.
 //
 // With block size 16 the key loop is software-pipelined: each wave issues the
-// next key tile's K/V loads before the current tile's math. The MFMA results
+// next key tile's K/V loads (buffer loads off a per-block descriptor) before the
+// current tile's math. The MFMA results
 // stay in VGPRs (built with -amdgpu-mfma-vgpr-form), so the per-tile rescale
 // and the softmax read them without accumulator-register copies.
 //
@@ -35,6 +36,7 @@
 // :234-242) and Attention.forward's masked softmax (tokquay/model.py:94-96).
 
 #include <hip/hip_ext.h>
+#include <float.h>
 #include <math.h>
 
 #include <algorithm>
@@ -79,6 +81,9 @@ struct PrefillArgs {
 };
 
 constexpr int kXcds = 8;      // MI355X: workgroup i is dispatched to XCD i % 8
+// Word 3 of a raw (untyped) buffer descriptor on gfx9-family GPUs: data format 32 bits (a
+// nonzero format makes the loads valid), no swizzle, no typed conversion.
+constexpr int kBufferWord3 = 0x00020000;
 constexpr int kRound = 64;    // dispatches per XCD taken as one round (two per CU of its 32)
 
 // Maps the dispatch index to a work tile. Workgroup p runs on XCD p % 8 (checked
@@ -160,11 +165,16 @@ __device__ __forceinline__ void load_kv_tile(const PrefillArgs& a, const int32_t
 // Max of v over the four lanes j, j + 16, j + 32, j + 48 (one query's lane groups), left in all
 // four: gfx950's cross-row lane swaps (v_permlane16_swap / v_permlane32_swap) on the VALU instead
 // of two LDS-unit permutes per key tile.
+// Maxima are IEEE maximum (v_maximum3_f32 / v_maximum_f32): unlike fmaxf they need no
+// canonicalization of their operands, and the scores hold no NaN.
+__device__ __forceinline__ float max2(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float max4(float a, float b, float c, float d) { return max2(max2(a, b), max2(c, d)); }
+
 __device__ __forceinline__ float max_over_lane_groups(float v) {
   const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = fmaxf(__uint_as_float(p16[0]), __uint_as_float(p16[1]));  // rows 0<->1, 2<->3
+  v = max2(__uint_as_float(p16[0]), __uint_as_float(p16[1]));  // rows 0<->1, 2<->3
   const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(p32[0]), __uint_as_float(p32[1]));  // lanes 0-31 <-> 32-63
+  return max2(__uint_as_float(p32[0]), __uint_as_float(p32[1]));  // lanes 0-31 <-> 32-63
 }
 
 // Same loads when a 16-key tile is exactly one block (block size 16): the tile's
@@ -210,8 +220,9 @@ __device__ __forceinline__ void load_kv_block_tile(const PrefillArgs& a, const f
 // of one sequence, or nothing for a padding workgroup. QH = 2 (one wave per workgroup only) feeds
 // each key tile's loads to twice the MFMAs and gives the wave two independent softmax chains.
 // PIPE: the software-pipelined key loop (block size 16 only). The mixed launch keeps the plain
-// loop: its decode workgroups share the kernel, and the pipelined loop's 130-138 VGPRs would hold
-// them to 3 waves per SIMD instead of 4 (config 5's chunk steps ran about 1 % slower with it).
+// loop: with the pipelined one (126 VGPRs, its decode workgroups still at 4 waves per SIMD) the
+// steps of four 256-token prompt chunks beside 128 decoding sequences ran from 3 % faster to 2 %
+// slower depending on the chunk.
 template <int BS_CT, int KS, int QH = 1, bool PIPE = (BS_CT == kTile)>
 __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int dispatch) {
   static_assert(!PIPE || BS_CT == kTile, "the pipelined key loop reads one block per key tile");
@@ -304,13 +315,17 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
   const float* head_base = a.pool_layer + (int64_t)h * a.head_stride;
   const int kend = start + min(qi0 + kTile * QH, nq);  // keys the wave's tiles can see: [0, kend)
 
+  // The running reference maximum m starts at the lowest finite float rather than -inf: a lane
+  // that has seen no key then computes p = 2^(-inf - m) = 0 with no special case, and its first
+  // visible score passes m + kSlack. mthr = m + kSlack is kept beside m.
   floatx4 o[QH][4];
-  float m[QH], l[QH];
+  float m[QH], mthr[QH], l[QH];
 #pragma unroll
   for (int u = 0; u < QH; ++u) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) o[u][t] = floatx4{0.f, 0.f, 0.f, 0.f};
-    m[u] = -INFINITY;
+    m[u] = -FLT_MAX;
+    mthr[u] = -FLT_MAX + kSlack;
     l[u] = 0.f;
   }
 
@@ -318,51 +333,61 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
   // operand K[kt + j][16g + s] and the PV A operand rows V[kt + 4g + s][4j .. 4j+3].
   // One key tile's math for each query tile: S^T = K Q^T, the online-softmax update,
   // O^T += V^T P^T.
+  //
+  // On gfx950 the fp32 MFMAs and the VALU do not overlap: every VALU instruction in the loop
+  // adds to the key tile's time (about 2.5-5 cycles each, v_exp_f32 about 10, against 32 per
+  // MFMA), while a chain of dependent MFMAs issues at the full rate. The step is written for
+  // the fewest VALU instructions: one MFMA chain per score tile (no partial sums to add), the
+  // running-maximum test on each lane's own four scores (the lane-group maximum only when some
+  // lane's test fires), max as v_maximum3_f32 (no operand canonicalization), and one ballot
+  // for all of the wave's query tiles.
   auto consume = [&](int kt, const float (&kreg)[16], const float4 (&vreg)[4]) {
-      // Two independent MFMA chains (even / odd dim groups) per query tile halve the dependent
-      // latency.
-      floatx4 st0[QH], st1[QH];
+      floatx4 st[QH];
   #pragma unroll
-      for (int u = 0; u < QH; ++u) st0[u] = st1[u] = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int u = 0; u < QH; ++u) st[u] = floatx4{0.f, 0.f, 0.f, 0.f};
   #pragma unroll
-      for (int s = 0; s < 16; s += 2) {
+      for (int s = 0; s < 16; ++s) {
+  #pragma unroll
+        for (int u = 0; u < QH; ++u) st[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(kreg[s], qreg[u][s], st[u], 0, 0, 0);
+      }
+      // sm[u][r] = S^T[key kt + 4g + r][query j] in log2 units, -inf past the diagonal.
+      float sm[QH][4], lmax[QH];
+      bool grow_any = false;
+  #pragma unroll
+      for (int u = 0; u < QH; ++u) {
+        if (kt + kTile - 1 > qpos_lo[u]) {  // uniform: the key tile crosses this query tile's diagonal
+  #pragma unroll
+          for (int r = 0; r < 4; ++r) sm[u][r] = kt + 4 * g + r <= qpos[u] ? st[u][r] : -INFINITY;
+        } else {
+  #pragma unroll
+          for (int r = 0; r < 4; ++r) sm[u][r] = st[u][r];
+        }
+        lmax[u] = max4(sm[u][0], sm[u][1], sm[u][2], sm[u][3]);
+        grow_any |= lmax[u] > mthr[u];
+      }
+      // Lazy rescale: the reference maximum m of a query moves only when one of its scores
+      // exceeds m + kSlack (log2 units), so p <= 2^kSlack and the accumulators are rescaled on
+      // few tiles. A query's maximum passes the threshold exactly when one of its four lanes'
+      // maxima does, so the per-lane test decides for the wave through the ballot.
+      if (__builtin_amdgcn_ballot_w64(grow_any) != 0) {
   #pragma unroll
         for (int u = 0; u < QH; ++u) {
-          st0[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(kreg[s], qreg[u][s], st0[u], 0, 0, 0);
-          st1[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(kreg[s + 1], qreg[u][s + 1], st1[u], 0, 0, 0);
+          const float tmax = max_over_lane_groups(lmax[u]);
+          const bool grow = tmax > mthr[u];
+          const float mn = grow ? tmax : m[u];
+          const float corr = grow ? __builtin_amdgcn_exp2f(m[u] - mn) : 1.f;  // first key: 0
+          l[u] *= corr;
+  #pragma unroll
+          for (int t = 0; t < 4; ++t) o[u][t] *= corr;
+          m[u] = mn;
+          mthr[u] = mn + kSlack;
         }
       }
       float p[QH][4];
   #pragma unroll
       for (int u = 0; u < QH; ++u) {
-        const floatx4 st = st0[u] + st1[u];  // st[r] = S^T[key kt + 4g + r][query j], log2 units
-        float sm[4];
-        if (kt + kTile - 1 > qpos_lo[u]) {  // uniform: the key tile crosses this query tile's diagonal
   #pragma unroll
-          for (int r = 0; r < 4; ++r) sm[r] = kt + 4 * g + r <= qpos[u] ? st[r] : -INFINITY;
-        } else {
-  #pragma unroll
-          for (int r = 0; r < 4; ++r) sm[r] = st[r];
-        }
-        float tmax = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
-        tmax = max_over_lane_groups(tmax);
-        // Lazy rescale: the reference maximum m moves only when a score exceeds it by
-        // more than kSlack (log2 units), so p <= 2^kSlack and the accumulators are
-        // rescaled on few tiles. The test is wave-uniform through the ballot.
-        const bool grow = tmax > m[u] + kSlack;  // false while the query has seen no key
-        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-          const float mn = grow ? tmax : m[u];
-          const float corr = grow ? __builtin_amdgcn_exp2f(m[u] - mn) : 1.f;  // m = -inf: 0
-          l[u] *= corr;
-  #pragma unroll
-          for (int t = 0; t < 4; ++t) o[u][t] *= corr;
-          m[u] = mn;
-        }
-        // A query with no visible key so far (m = -inf) has only -inf scores here:
-        // any finite reference gives p = 0 and keeps its state exactly zero.
-        const float mref = m[u] == -INFINITY ? 0.f : m[u];
-  #pragma unroll
-        for (int r = 0; r < 4; ++r) p[u][r] = __builtin_amdgcn_exp2f(sm[r] - mref);
+        for (int r = 0; r < 4; ++r) p[u][r] = __builtin_amdgcn_exp2f(sm[u][r] - m[u]);
         l[u] += (p[u][0] + p[u][1]) + (p[u][2] + p[u][3]);
       }
 
@@ -389,6 +414,15 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
     // block 0); keys past kend or in a bad block are zeroed after they arrive.
     int tb_base = -1;
     int32_t tb_id = 0;
+    // Byte offsets inside a block of lane (j, g)'s K row part (position j, dims 16g ..) and of
+    // its first V row (position 4g, dims 4j ..), with the K-to-V distance folded into the latter.
+    // The tile's loads are buffer loads off a descriptor on the block (scalar registers) with
+    // these loop-invariant offsets: no per-tile 64-bit address arithmetic on the VALU. The
+    // descriptor spans the block's K tile through the end of its V tile.
+    const uint32_t kv_bytes = (uint32_t)(a.kv_stride * (int64_t)sizeof(float));
+    const uint32_t k_off = (uint32_t)(j * kHeadDim + 16 * g) * 4u;
+    const uint32_t v_off = kv_bytes + (uint32_t)(4 * g * kHeadDim + 4 * j) * 4u;
+    const int32_t rsrc_bytes = (int32_t)(kv_bytes + kTile * kHeadDim * 4u);
     auto fetch = [&](int kt, float (&kreg)[16], float4 (&vreg)[4]) -> int32_t {
       const int ti = kt / kTile;
       if ((ti & ~63) != tb_base) {  // wave-uniform
@@ -402,19 +436,20 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
         }
       }
       const int32_t blk = __builtin_amdgcn_readlane(tb_id, ti - tb_base);
-      const float* base = head_base + (int64_t)(blk < 0 ? 0 : blk) * a.block_stride;
-      const float* kp = base + j * kHeadDim + 16 * g;
+      const float* kb = head_base + (int64_t)(blk < 0 ? 0 : blk) * a.block_stride;
+      const __amdgpu_buffer_rsrc_t rsrc =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(kb), (short)0, rsrc_bytes, kBufferWord3);
 #pragma unroll
       for (int v4 = 0; v4 < 4; ++v4) {
-        const float4 x = *reinterpret_cast<const float4*>(kp + 4 * v4);
-        kreg[4 * v4 + 0] = x.x;
-        kreg[4 * v4 + 1] = x.y;
-        kreg[4 * v4 + 2] = x.z;
-        kreg[4 * v4 + 3] = x.w;
+        const auto x = __builtin_amdgcn_raw_buffer_load_b128(rsrc, k_off + 16u * v4, 0, 0);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) kreg[4 * v4 + c] = __uint_as_float(x[c]);
       }
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        vreg[s] = *reinterpret_cast<const float4*>(base + a.kv_stride + (4 * g + s) * kHeadDim + 4 * j);
+      for (int s = 0; s < 4; ++s) {
+        const auto x = __builtin_amdgcn_raw_buffer_load_b128(rsrc, v_off + (uint32_t)(s * kHeadDim * 4), 0, 0);
+        vreg[s] = make_float4(__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]), __uint_as_float(x[3]));
+      }
       return blk;
     };
     // Zero what must not count (uniform test; only the last tile or a bad block).
@@ -545,7 +580,7 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
 #pragma unroll
       for (int w = 0; w < KS; ++w) {
         const float mw = s_ml[w][0][j];
-        const float cw = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);  // waves that saw no key weigh 0
+        const float cw = __builtin_amdgcn_exp2f(mw - M);  // a wave that saw no key (m = -FLT_MAX) weighs 0
         L = fmaf(s_ml[w][1][j], cw, L);
         acc.x = fmaf(s_o[w][lane][4 * part + 0], cw, acc.x);
         acc.y = fmaf(s_o[w][lane][4 * part + 1], cw, acc.y);
@@ -585,15 +620,16 @@ void launch_prefill_ks(const PrefillArgs& a, hipStream_t stream, hipEvent_t star
 
 // Waves per workgroup: the largest key split KS that still lets every workgroup of
 // the launch be resident at once (a second round of workgroups costs more than the
-// split saves). The pipelined kernel holds 3 waves per SIMD, so a CU takes 12 / KS of
-// its workgroups: KS = 4 up to 768 tiles, 2 up to 1536. The KS = 8 instance takes one
+// split saves). The bounds count 12 wave slots per CU (3 waves per SIMD), so a CU takes
+// 12 / KS of the workgroups: KS = 4 up to 768 tiles, 2 up to 1536. (The pipelined kernel now
+// fits 4 waves per SIMD; 16 slots timed the same on the chunk shapes.) The KS = 8 instance takes one
 // workgroup per CU (its LDS reservation): up to 256 tiles. Measured on 256-token chunks:
 // 768 tiles run best with 4, 960 with 2, 576 with 4; KS = 16 (plain loop) on 192-252
 // tiles ran 15-20 % slower than 8; the pipelined loop at KS = 8 took a 3-prompt tail
 // chunk with 5 / 102 / 9 rows at position 768 from 15.1 to 13.8 us.
 int choose_key_split(int64_t tiles) {
   constexpr int kCus = 256;
-  constexpr int kSlotsPipelined = 12;  // wave slots per CU at 3 waves per SIMD
+  constexpr int kSlotsPipelined = 12;  // wave slots per CU counted at 3 waves per SIMD
   if (tiles <= kCus) return 8;
   for (int ks = 4; ks > 1; ks /= 2)
     if (tiles <= (int64_t)kCus * (kSlotsPipelined / ks)) return ks;
@@ -680,6 +716,9 @@ tq_status make_prefill_args(const PrefillCall& c, PrefillArgs& a, bool& empty) {
   if ((int64_t)c.max_blocks_per_seq * c.block_size > 0x7fffffffLL) return TQ_ERR_UNSUPPORTED;
 
   const PoolGeom g = pool_geom(c.num_layers, c.num_heads, c.block_size, c.head_dim, c.layer);
+  // The block-size-16 key loop addresses a block's K and V tiles with 32-bit byte offsets.
+  if (g.kv_stride * (int64_t)sizeof(float) + kTile * kHeadDim * (int64_t)sizeof(float) > 0x7fffffffLL)
+    return TQ_ERR_UNSUPPORTED;
   a = PrefillArgs{};
   a.out = c.out;
   a.out_stride = c.out_row_stride;
