@@ -648,8 +648,8 @@ def test_other_head_counts(n_head, kind):
 @pytest.mark.parametrize("block_size", [8, 16])
 @pytest.mark.parametrize("num_seqs", [1, 3, 40])
 def test_prefill_bad_block_id_is_reported_and_contained(block_size, num_seqs):
-    """A block-table entry outside the pool is reported (TQ_DEVERR_BLOCK_ID); the kernel reads block 0
-    in its place and zeroes it, so the bad sequence's rows stay finite and every other sequence's rows
+    """A block-table entry outside the pool is reported (TQ_DEVERR_BLOCK_ID); the kernel takes zeros for
+    that block's keys and values, so the bad sequence's rows stay finite and every other sequence's rows
     are bit-identical to a launch with a valid table (1 / 3 / 40 sequences: 8 / 4 / 1 waves per query
     tile)."""
     from tokquay_amd import _lib, ops

@@ -177,42 +177,35 @@ __device__ __forceinline__ float max_over_lane_groups(float v) {
   return max2(__uint_as_float(p32[0]), __uint_as_float(p32[1]));  // lanes 0-31 <-> 32-63
 }
 
-// Same loads when a 16-key tile is exactly one block (block size 16): the tile's
-// block id arrives as a wave-uniform scalar (blk < 0: out of range, load zeros).
-__device__ __forceinline__ void load_kv_block_tile(const PrefillArgs& a, const float* head_base, int64_t blk,
+// Same loads when a 16-key tile is exactly one block (block size 16): the tile's block id arrives
+// as a wave-uniform scalar (blk < 0: out of range). They are buffer loads off two descriptors
+// built on the block's K and V tiles (scalar registers), with fixed per-lane byte offsets: lane
+// (j, g) reads K row j (dims 16g ..) and V rows 4g .. 4g + 3 (dims 4j ..), so no per-tile 64-bit
+// address arithmetic runs on the VALU. The descriptors' sizes do the masking: they cover the
+// tile's rows below kend (none for a bad block id), and the hardware returns zeros for every load
+// past them, which is what the keys past the range and a bad block must contribute.
+__device__ __forceinline__ void load_kv_block_tile(const PrefillArgs& a, const float* head_base, int32_t blk,
                                                    int kt, int kend, int j, int g, float (&kreg)[16],
                                                    float4 (&vreg)[4]) {
-  const float* base = head_base + (blk < 0 ? 0 : blk) * a.block_stride;
-  if (blk >= 0 && kt + kTile <= kend) {  // uniform: every key of the tile is valid, nothing to mask
-    const float* kp = base + j * kHeadDim + 16 * g;
-#pragma unroll
-    for (int v4 = 0; v4 < 4; ++v4) {
-      const float4 x = *reinterpret_cast<const float4*>(kp + 4 * v4);
-      kreg[4 * v4 + 0] = x.x;
-      kreg[4 * v4 + 1] = x.y;
-      kreg[4 * v4 + 2] = x.z;
-      kreg[4 * v4 + 3] = x.w;
-    }
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-      vreg[s] = *reinterpret_cast<const float4*>(base + a.kv_stride + (4 * g + s) * kHeadDim + 4 * j);
-    return;
-  }
-  const bool k_ok = blk >= 0 && kt + j < kend;
-  const float* kp = base + j * kHeadDim + 16 * g;
+  constexpr int kRowBytes = kHeadDim * 4;
+  const uint32_t k_off = (uint32_t)(j * kHeadDim + 16 * g) * 4u;
+  const uint32_t v_off = (uint32_t)(4 * g * kHeadDim + 4 * j) * 4u;
+  const int rows = blk < 0 ? 0 : min(kTile, kend - kt);  // uniform: rows that count
+  const float* kb = head_base + (int64_t)(blk < 0 ? 0 : blk) * a.block_stride;
+  const __amdgpu_buffer_rsrc_t kd =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(kb), (short)0, rows * kRowBytes, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t vd = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(kb + a.kv_stride),
+                                                                      (short)0, rows * kRowBytes, kBufferWord3);
 #pragma unroll
   for (int v4 = 0; v4 < 4; ++v4) {
-    const float4 x = k_ok ? *reinterpret_cast<const float4*>(kp + 4 * v4) : make_float4(0.f, 0.f, 0.f, 0.f);
-    kreg[4 * v4 + 0] = x.x;
-    kreg[4 * v4 + 1] = x.y;
-    kreg[4 * v4 + 2] = x.z;
-    kreg[4 * v4 + 3] = x.w;
+    const auto x = __builtin_amdgcn_raw_buffer_load_b128(kd, k_off + 16u * v4, 0, 0);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) kreg[4 * v4 + c] = __uint_as_float(x[c]);
   }
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    const bool v_ok = blk >= 0 && kt + 4 * g + s < kend;
-    vreg[s] = v_ok ? *reinterpret_cast<const float4*>(base + a.kv_stride + (4 * g + s) * kHeadDim + 4 * j)
-                   : make_float4(0.f, 0.f, 0.f, 0.f);
+    const auto x = __builtin_amdgcn_raw_buffer_load_b128(vd, v_off + (uint32_t)(s * kRowBytes), 0, 0);
+    vreg[s] = make_float4(__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]), __uint_as_float(x[3]));
   }
 }
 
@@ -409,21 +402,10 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
     // v_readlane (no table loads in the loop); the lane copy is refreshed when the
     // wave moves to the next 64.
     // The loop is software-pipelined over two register buffers: the next tile's
-    // K/V loads are issued before the current tile's math. Loads are unconditional
-    // (a tile is one whole block, so every address is inside it; a bad id reads
-    // block 0); keys past kend or in a bad block are zeroed after they arrive.
+    // K/V loads are issued before the current tile's math.
     int tb_base = -1;
     int32_t tb_id = 0;
-    // Byte offsets inside a block of lane (j, g)'s K row part (position j, dims 16g ..) and of
-    // its first V row (position 4g, dims 4j ..), with the K-to-V distance folded into the latter.
-    // The tile's loads are buffer loads off a descriptor on the block (scalar registers) with
-    // these loop-invariant offsets: no per-tile 64-bit address arithmetic on the VALU. The
-    // descriptor spans the block's K tile through the end of its V tile.
-    const uint32_t kv_bytes = (uint32_t)(a.kv_stride * (int64_t)sizeof(float));
-    const uint32_t k_off = (uint32_t)(j * kHeadDim + 16 * g) * 4u;
-    const uint32_t v_off = kv_bytes + (uint32_t)(4 * g * kHeadDim + 4 * j) * 4u;
-    const int32_t rsrc_bytes = (int32_t)(kv_bytes + kTile * kHeadDim * 4u);
-    auto fetch = [&](int kt, float (&kreg)[16], float4 (&vreg)[4]) -> int32_t {
+    auto fetch = [&](int kt, float (&kreg)[16], float4 (&vreg)[4]) {
       const int ti = kt / kTile;
       if ((ti & ~63) != tb_base) {  // wave-uniform
         tb_base = ti & ~63;
@@ -435,43 +417,14 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
           else flag_error(a.d_error, TQ_DEVERR_BLOCK_ID);
         }
       }
-      const int32_t blk = __builtin_amdgcn_readlane(tb_id, ti - tb_base);
-      const float* kb = head_base + (int64_t)(blk < 0 ? 0 : blk) * a.block_stride;
-      const __amdgpu_buffer_rsrc_t rsrc =
-          __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(kb), (short)0, rsrc_bytes, kBufferWord3);
-#pragma unroll
-      for (int v4 = 0; v4 < 4; ++v4) {
-        const auto x = __builtin_amdgcn_raw_buffer_load_b128(rsrc, k_off + 16u * v4, 0, 0);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) kreg[4 * v4 + c] = __uint_as_float(x[c]);
-      }
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const auto x = __builtin_amdgcn_raw_buffer_load_b128(rsrc, v_off + (uint32_t)(s * kHeadDim * 4), 0, 0);
-        vreg[s] = make_float4(__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]), __uint_as_float(x[3]));
-      }
-      return blk;
-    };
-    // Zero what must not count (uniform test; only the last tile or a bad block).
-    auto mask = [&](int kt, int32_t blk, float (&kreg)[16], float4 (&vreg)[4]) {
-      if (blk < 0 || kt + kTile > kend) {
-        const bool k_ok = blk >= 0 && kt + j < kend;
-#pragma unroll
-        for (int s = 0; s < 16; ++s) kreg[s] = k_ok ? kreg[s] : 0.f;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const bool v_ok = blk >= 0 && kt + 4 * g + s < kend;
-          vreg[s] = v_ok ? vreg[s] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-      }
+      load_kv_block_tile(a, head_base, __builtin_amdgcn_readlane(tb_id, ti - tb_base), kt, kend, j, g, kreg, vreg);
     };
     const int step = KS * kTile;
     int kt = wave * kTile;
     const bool any = kt < kend;  // wave-uniform
     float ka[16], kb[16];
     float4 va[4], vb[4];
-    int32_t ba = -1, bb;
-    if (any) ba = fetch(kt, ka, va);
+    if (any) fetch(kt, ka, va);
     if constexpr (kSharedQ) {
       // Every wave, also one with no key tile, stages its Q columns; then all read the tile.
       __shared__ float s_q[kTile][kHeadDim];
@@ -495,16 +448,14 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
         // Always issue the next loads (the last tile re-reads itself), so the wait
         // counts before each tile's math are the same on every path.
         const bool more = kt + step < kend;  // uniform
-        bb = fetch(more ? kt + step : kt, kb, vb);
+        fetch(more ? kt + step : kt, kb, vb);
         __builtin_amdgcn_sched_barrier(0);
-        mask(kt, ba, ka, va);
         consume(kt, ka, va);
         if (!more) break;
         kt += step;
         const bool more2 = kt + step < kend;
-        ba = fetch(more2 ? kt + step : kt, ka, va);
+        fetch(more2 ? kt + step : kt, ka, va);
         __builtin_amdgcn_sched_barrier(0);
-        mask(kt, bb, kb, vb);
         consume(kt, kb, vb);
         if (!more2) break;
         kt += step;
@@ -528,8 +479,7 @@ __device__ __forceinline__ void prefill_workgroup(const PrefillArgs& a, int disp
             else flag_error(a.d_error, TQ_DEVERR_BLOCK_ID);
           }
         }
-        const int64_t blk = __builtin_amdgcn_readlane(tb_id, ti - tb_base);
-        load_kv_block_tile(a, head_base, blk, kt, kend, j, g, kreg, vreg);
+        load_kv_block_tile(a, head_base, __builtin_amdgcn_readlane(tb_id, ti - tb_base), kt, kend, j, g, kreg, vreg);
       } else {
         load_kv_tile<BS_CT>(a, bt, head_base, bs, kt, kend, j, g, kreg, vreg);
       }
@@ -716,9 +666,6 @@ tq_status make_prefill_args(const PrefillCall& c, PrefillArgs& a, bool& empty) {
   if ((int64_t)c.max_blocks_per_seq * c.block_size > 0x7fffffffLL) return TQ_ERR_UNSUPPORTED;
 
   const PoolGeom g = pool_geom(c.num_layers, c.num_heads, c.block_size, c.head_dim, c.layer);
-  // The block-size-16 key loop addresses a block's K and V tiles with 32-bit byte offsets.
-  if (g.kv_stride * (int64_t)sizeof(float) + kTile * kHeadDim * (int64_t)sizeof(float) > 0x7fffffffLL)
-    return TQ_ERR_UNSUPPORTED;
   a = PrefillArgs{};
   a.out = c.out;
   a.out_stride = c.out_row_stride;
