@@ -549,6 +549,37 @@ def test_prefill_two_query_tiles_per_wave_edges():
     check(sc, brute=False)
 
 
+@pytest.mark.parametrize("shape", ["key_split", "two_tiles"])
+@pytest.mark.parametrize("scores", ["wide", "all_negative"])
+def test_prefill_running_maximum_over_wide_score_ranges(shape, scores):
+    """The lazy running maximum under score ranges that move it often: q scaled so that scores spread
+    over tens of log2 units (the maximum grows on many key tiles, the per-lane test firing for some
+    lanes of a wave only), and every score of every query far below zero (keys share a direction q
+    points against: the first visible key sets the maximum, no probability underflows). Both the
+    key-split launch (4 prompts) and the two-query-tiles-per-wave launch (8,316 row tiles), against
+    the reference."""
+    rng = random.Random(31)
+    if shape == "key_split":
+        lens = [256, 200, 131, 77]
+        starts = [0, 100, 16, 300]
+    else:
+        base = [2, 15, 16, 17, 31, 32, 33, 47, 48, 49, 64, 65]
+        lens = [base[i % len(base)] for i in range(320)]
+        starts = [rng.choice([0, 5, 16, 100]) for _ in lens]
+    sc = Scenario(starts, lens, block_size=16, seed=41)
+    if scores == "wide":
+        sc.q *= 8.0
+    else:
+        u = torch.randn(64, generator=torch.Generator().manual_seed(42))
+        u = u / u.norm()
+        for tbl, s in zip(sc.tables, sc.starts):  # the cached keys: + 6 u
+            for p in range(s):
+                sc.pool[tbl[p // 16], 0, 0, :, p % 16] += 6.0 * u
+        sc.k += 6.0 * u
+        sc.q = sc.q * 0.1 - 50.0 * u  # scores about -300 / 8 = -37.5 natural units, all negative
+    check(sc, brute=shape == "key_split")
+
+
 @pytest.mark.parametrize("num_seqs,max_len", [(80, 400), (40, 300), (4, 256)])
 def test_prefill_dispatch_order_does_not_change_results(num_seqs, max_len):
     """seq_order only changes how a launch deals its sequences: identical bits for no order, the
