@@ -59,7 +59,7 @@ N_SEQS, CTX_LO, CTX_HI, BLOCK, POOL_BLOCKS = 256, 256, 1024, 16, 16384
 N_HEAD, D_HEAD = 12, 64
 # HBM bytes the decode kernel moves per algorithmic byte on this workload, from two rocprofv3
 # counter runs on ``bench.py --pmc-probe`` (FETCH_SIZE scaled x2.0 and WRITE_SIZE x1.0, the factors
-# a 1 GiB copy kernel of known size gives): 999.96 MB read + 2.36 MB written per launch for
+# a 1 GiB copy kernel of known size gives): 999.95 MB read + 2.36 MB written per launch for
 # 996.43 MB algorithmic (an earlier pair of runs on another box read 1,008.00 MB: 1.0140). The
 # excess is the masked tail of each wave's last 16-position chunk.
 DECODE_TRAFFIC_PER_ALGO_BYTE = 1.0059
