@@ -27,10 +27,10 @@
 // accumulators are rescaled, only when a score passes it by more than 2^8.
 //
 // With block size 16 the key loop is software-pipelined: each wave issues the
-// next key tile's K/V loads (buffer loads off a per-block descriptor) before the
-// current tile's math. The MFMA results
-// stay in VGPRs (built with -amdgpu-mfma-vgpr-form), so the per-tile rescale
-// and the softmax read them without accumulator-register copies.
+// next key tile's K/V loads (buffer loads off descriptors on the block's K and V
+// tiles) before the current tile's math. The MFMA results stay in VGPRs (built
+// with -amdgpu-mfma-vgpr-form), so the per-tile rescale and the softmax read them
+// without accumulator-register copies.
 //
 // Reference semantics: PagedBatch.gather + mask (tokquay/kv_cache.py:208-214,
 // :234-242) and Attention.forward's masked softmax (tokquay/model.py:94-96).
@@ -162,14 +162,14 @@ __device__ __forceinline__ void load_kv_tile(const PrefillArgs& a, const int32_t
   }
 }
 
-// Max of v over the four lanes j, j + 16, j + 32, j + 48 (one query's lane groups), left in all
-// four: gfx950's cross-row lane swaps (v_permlane16_swap / v_permlane32_swap) on the VALU instead
-// of two LDS-unit permutes per key tile.
 // Maxima are IEEE maximum (v_maximum3_f32 / v_maximum_f32): unlike fmaxf they need no
-// canonicalization of their operands, and the scores hold no NaN.
+// canonicalization of their operands, and a NaN score propagates instead of being dropped.
 __device__ __forceinline__ float max2(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 __device__ __forceinline__ float max4(float a, float b, float c, float d) { return max2(max2(a, b), max2(c, d)); }
 
+// Max of v over the four lanes j, j + 16, j + 32, j + 48 (one query's lane groups), left in all
+// four: gfx950's cross-row lane swaps (v_permlane16_swap / v_permlane32_swap) on the VALU instead
+// of two LDS-unit permutes per key tile.
 __device__ __forceinline__ float max_over_lane_groups(float v) {
   const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   v = max2(__uint_as_float(p16[0]), __uint_as_float(p16[1]));  // rows 0<->1, 2<->3
