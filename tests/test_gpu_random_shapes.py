@@ -64,3 +64,33 @@ def test_random_batch_matches_the_reference(seed):
         for r, flat in enumerate(batch.token_index.cpu().tolist()):
             b, t = divmod(flat, T)
             np.testing.assert_allclose(got[r], exact[b][t], rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_mixed_step_one_launch_equals_two_launches(seed):
+    """Random batch views that hold both decode rows and multi-token rows, at an explicit decode
+    partition length: the one-launch mixed kernel gives the two single-kind launches' bits (outputs
+    and pool)."""
+    from tokquay_amd.kv_cache import PagedBatch
+
+    rng = random.Random(5000 + seed)
+    shape, starts, lens = draw(5000 + seed)
+    starts.append(rng.randint(1, 900))  # at least one decode row and one chunk
+    lens.append(1)
+    starts.append(rng.randint(0, 400))
+    lens.append(rng.randint(2, 200))
+    part = rng.choice([64, 256, 1024])
+    print(f"seed {seed}: {shape}, partition {part}, starts {starts}, new lengths {lens}", flush=True)
+    sc = Scenario(starts, lens, block_size=shape["block_size"], n_layer=shape["n_layer"], layer=shape["layer"],
+                  seed=7000 + seed, n_head=shape["n_head"])
+    res = []
+    try:
+        for one in (False, True):
+            PagedBatch.one_launch_mixed = one
+            res.append(sc.run_product(part))
+    finally:
+        PagedBatch.one_launch_mixed = True
+    (pool_a, out_a, batch), (pool_b, out_b, _) = res
+    assert batch.num_decode > 0 and batch.num_prefill > 0
+    assert torch.equal(out_a, out_b)
+    assert torch.equal(pool_a, pool_b)
