@@ -94,3 +94,48 @@ def test_random_mixed_step_one_launch_equals_two_launches(seed):
     assert batch.num_decode > 0 and batch.num_prefill > 0
     assert torch.equal(out_a, out_b)
     assert torch.equal(pool_a, pool_b)
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_random_decode_write_equals_cache_write_then_decode(seed):
+    """Random decode batches (1-64 rows, contexts 0-1,500 where 0 is a padding row, block sizes 1-64,
+    1-25 heads, automatic or explicit partitions): tq_paged_decode_write gives the bits of
+    tq_cache_write followed by tq_paged_decode, output and pool."""
+    from tokquay_amd import ops
+
+    rng = random.Random(9000 + seed)
+    bs = rng.choice(BLOCK_SIZES)
+    heads = rng.choice(HEADS)
+    part = rng.choice([0, 0, 16, 64, 256, 1024])
+    ctx = [rng.choice([0, rng.randint(1, 1500), rng.randint(1, 64)]) for _ in range(rng.randint(1, 64))]
+    ctx[0] = max(ctx[0], 1)
+    print(f"seed {seed}: block {bs}, heads {heads}, partition {part}, contexts {ctx}", flush=True)
+    n_layer, layer = 2, rng.randrange(2)
+    cdiv = lambda a, b: -(-a // b)  # noqa: E731
+    nb = sum(cdiv(c, bs) for c in ctx) + 2
+    C = heads * 64
+    pool0 = torch.randn(nb, n_layer, 2, heads, bs, 64, generator=torch.Generator().manual_seed(seed)) * 50
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(seed + 1)).tolist()
+    maxc = max(ctx)
+    width = cdiv(maxc, bs)
+    tables = torch.zeros(len(ctx), width, dtype=torch.int32)
+    slots, i = [], 0
+    for b, c in enumerate(ctx):
+        n = cdiv(c, bs)
+        tables[b, :n] = torch.tensor(perm[i : i + n], dtype=torch.int32)
+        i += n
+        slots.append(int(tables[b, (c - 1) // bs]) * bs + (c - 1) % bs if c else -1)
+    qkv = torch.randn(len(ctx), 3 * C, generator=torch.Generator().manual_seed(seed + 2)).cuda()
+    q, k, v = qkv[:, :C], qkv[:, C : 2 * C], qkv[:, 2 * C :]
+    tables, cl = tables.cuda(), torch.tensor(ctx, dtype=torch.int32, device="cuda")
+    sm = torch.tensor(slots, dtype=torch.int64, device="cuda")
+    pa, pb = pool0.cuda(), pool0.cuda()
+    oa, ob = torch.empty(len(ctx), C, device="cuda"), torch.empty(len(ctx), C, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ops.cache_write(pa, layer, k, v, sm, err)
+    ops.paged_decode(oa, q, pa, layer, tables, cl, maxc, partition_tokens=part, d_error=err)
+    ops.paged_decode(ob, q, pb, layer, tables, cl, maxc, partition_tokens=part, d_error=err, k_new=k, v_new=v)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    assert torch.equal(oa, ob)
+    assert torch.equal(pa, pb)
