@@ -139,3 +139,45 @@ def test_random_decode_write_equals_cache_write_then_decode(seed):
     assert int(err.item()) == 0
     assert torch.equal(oa, ob)
     assert torch.equal(pa, pb)
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_random_prefill_dispatch_order_keeps_the_bits(seed):
+    """Random prompt and chunk batches large enough for one-wave launches (one or two query tiles per
+    wave, block size 16): the natural order, most causal work first and a random permutation give
+    the same bits."""
+    from tokquay_amd import ops
+
+    rng = random.Random(11000 + seed)
+    n = rng.randint(40, 160)
+    lens = [rng.randint(1, rng.choice([64, 300, 700])) for _ in range(n)]
+    starts = [rng.choice([0, 0, rng.randint(1, 300)]) for _ in range(n)]
+    print(f"seed {seed}: {n} sequences, {sum(lens)} rows", flush=True)
+    cdiv = lambda a, b: -(-a // b)  # noqa: E731
+    ctx = [s + m for s, m in zip(starts, lens)]
+    nb = sum(cdiv(c, 16) for c in ctx) + 4
+    pool = torch.randn(nb, 1, 2, 12, 16, 64, generator=torch.Generator().manual_seed(seed)).cuda()
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(seed + 1)).tolist()
+    tables = torch.zeros(n, max(cdiv(c, 16) for c in ctx), dtype=torch.int32)
+    i = 0
+    for b, c in enumerate(ctx):
+        tables[b, : cdiv(c, 16)] = torch.tensor(perm[i : i + cdiv(c, 16)], dtype=torch.int32)
+        i += cdiv(c, 16)
+    cu_l = [0]
+    for m in lens:
+        cu_l.append(cu_l[-1] + m)
+    tables = tables.cuda()
+    cu = torch.tensor(cu_l, dtype=torch.int32, device="cuda")
+    st = torch.tensor(starts, dtype=torch.int32, device="cuda")
+    q = torch.randn(cu_l[-1], 768, generator=torch.Generator().manual_seed(seed + 2)).cuda()
+    work = [m * (2 * s + m + 1) for s, m in zip(starts, lens)]
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    outs = []
+    for order in (None, sorted(range(n), key=lambda b: -work[b]), rng.sample(range(n), n)):
+        out = torch.empty_like(q)
+        so = None if order is None else torch.tensor(order, dtype=torch.int32, device="cuda")
+        ops.paged_prefill(out, q, pool, 0, tables, cu, st, max(lens), d_error=err, seq_order=so)
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
